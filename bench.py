@@ -1,0 +1,181 @@
+"""Benchmark: tree-masked prefill attention on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline]
+
+One step is one ``dan_amd.attend`` call (one fused kernel launch) over the
+whole packed batch, inputs resident in HBM. The default workload is the
+Llama-3-8B attention shape (32 q / 8 kv heads, head_dim 128, bf16) at the
+8192-token serving budget with a shared 1024-token prefix-cache block
+(seed 0: 5 requests, 45 branches).
+
+Prints one JSON line:
+  value         useful TFLOP/s: 4 * D * H * (visible query-key pairs) / step time
+  tokens_per_s  packed tokens per second
+  roofline      the fused kernel against the bf16 dense matrix-core peak, from
+                HIP events around each launch on the launch stream
+  cpu_baseline  the masked CPU path (oracle restatement of the reference's
+                dense path, fp32, torch SDPA) on this host's cores
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 2516.6, "fp8": 5033.2}  # dense matrix-core peaks
+HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def useful_flops(w):
+    from oracle.tree_attention import useful_pairs  # same closed form for GPU and CPU
+
+    return 4 * w.q.shape[2] * w.q.shape[0] * useful_pairs(w.segments)
+
+
+def algorithmic_bytes(w):
+    """Q + K + V + O once, plus each distinct past tensor once."""
+    h, n, d = w.q.shape
+    hkv = w.k.shape[0]
+    es = w.q.element_size()
+    total = (2 * n * h * d + 2 * n * hkv * d) * es
+    seen = set()
+    for s in w.segments:
+        if s.past and id(s.past) not in seen:
+            seen.add(id(s.past))
+            pk, pv = s.past[w.layer][:2]
+            total += pk.numel() * pk.element_size() + pv.numel() * pv.element_size()
+    return total
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(name, seed, flops, n_tokens):
+    """Oracle (reference dense path restated) on the host: 1 warm-up, median of 3."""
+    from dan_amd import workloads
+    from oracle.tree_attention import attend_dense
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    w = workloads.CONFIGS[name](seed, device="cpu")
+    attend_dense(w.q, w.k, w.v, w.segments, w.layer)
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        attend_dense(w.q, w.k, w.v, w.segments, w.layer)
+        times.append(time.perf_counter() - t)
+    t = statistics.median(times)
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"full {name} seed {seed} workload ({n_tokens} packed tokens), fp32 torch SDPA per segment, "
+                      f"1 warm-up then median of 3 runs ({t:.3f} s); CPU: {cpu_model()}",
+            "seconds": round(t, 4), "tokens_per_s": round(n_tokens / t, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the tree-attention path runs on a single device "
+              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    from dan_amd import _native, workloads
+    from dan_amd.attention import attend
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    w = workloads.CONFIGS[args.workload](args.seed, device=dev)
+    flops = useful_flops(w)
+    nbytes = algorithmic_bytes(w)
+    n = w.num_tokens
+    dtype = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w.q.dtype]
+
+    out = None
+    for _ in range(args.warmup):
+        out = attend(w.q, w.k, w.v, w.segments, w.layer)
+    torch.cuda.synchronize()
+    if out is not None and not torch.isfinite(out).all():
+        raise RuntimeError("non-finite output")
+
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        attend(w.q, w.k, w.v, w.segments, w.layer)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    k_avg = statistics.mean(kernel_ms)
+    k_med = statistics.median(kernel_ms)
+
+    achieved = flops / (k_avg * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[dtype]
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get(f"{args.workload}_seed{args.seed}", {}).get("bytes_per_launch")
+
+    line = {
+        "metric": "tree-masked prefill attn TFLOP/s (useful) + packed tok/s, 8B shape, 1 GPU",
+        "value": round(flops / (ms_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "tokens_per_s": round(n / (ms_step * 1e-3), 1),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: " + (workloads.CONFIGS[args.workload].__doc__ or "").split(";")[0]
+                   .strip().replace("\n", " "),
+                   "seed": args.seed, "packed_tokens": n, "heads": f"{w.q.shape[0]}/{w.k.shape[0]}",
+                   "head_dim": w.q.shape[2], **{k: v for k, v in w.meta.items() if k != "packed_tokens"},
+                   "useful_gflop": round(flops / 1e9, 3), "algorithmic_mb": round(nbytes / 1e6, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "kernel_ms_avg": round(k_avg, 4), "kernel_ms_median": round(k_med, 4),
+                     "hbm_gbps_algorithmic": round(nbytes / (k_avg * 1e-3) / 1e9, 1),
+                     "hbm_frac_algorithmic": round(nbytes / (k_avg * 1e-3) / 1e9 / HBM_GBPS, 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.workload, args.seed, flops, n)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

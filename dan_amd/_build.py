@@ -1,0 +1,61 @@
+"""Build recipe for the gfx950 shared library (hipcc, in-tree).
+
+    python -m dan_amd._build          # -> dan_amd/_lib/libdan_tree_attn.so
+
+Flags:
+  --offload-arch=gfx950            CDNA4 only, no other targets.
+  -mcode-object-version=5          accepted by every ROCm 6/7 runtime (torch
+                                   ships its own HIP runtime).
+  -target-feature -packed-fp32-ops no packed fp32 VALU instructions.
+  -amdgpu-mfma-vgpr-form           matrix-core results in VGPRs, so the softmax
+                                   reads the score tile without AGPR copies.
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SRC = os.path.join(HERE, "csrc", "tree_attn.hip")
+INCLUDE = os.path.join(ROOT, "include")
+OUT_DIR = os.path.join(HERE, "_lib")
+OUT = os.path.join(OUT_DIR, "libdan_tree_attn.so")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-Wall", "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc():
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (ROCm is required to build the gfx950 library)")
+    return path
+
+
+def build(out=OUT, extra=(), verbose=False):
+    """Compile the library; always recompiles. Returns the output path."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", INCLUDE, SRC, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless.
+    noise = "is not a recognized feature for this target"
+    diag = "\n".join(line for line in (res.stderr or "").splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{diag}")
+    if diag.strip() and verbose:
+        print(diag, file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,115 @@
+"""ctypes binding of the C ABI in include/dan_tree_attn.h.
+
+The shared library is plain C ABI (no torch types), built in-tree by
+``dan_amd._build`` into ``dan_amd/_lib/``. It must be loaded after torch has
+initialised its HIP runtime: torch's bundled ``libamdhip64.so`` carries the
+soname the library links against, so both share one runtime and torch's
+stream handles are valid in it.
+
+There is no fallback: if the library is missing or cannot be loaded, every
+entry point raises.
+"""
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "_lib")
+LIB_NAME = "libdan_tree_attn.so"
+LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
+
+ABI_VERSION = 1
+KEY_TILE = 64
+
+# DanStatus
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_VERSION = range(5)
+# DanDtype
+DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_E4M3 = range(4)
+
+_i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class DanSegmentDesc(ctypes.Structure):
+    _fields_ = [("start", _i32), ("n", _i32), ("trunk", _i32), ("past_len", _i32), ("past_idx", _i32),
+                ("reserved", _i32 * 3)]
+
+
+class DanPastDesc(ctypes.Structure):
+    _fields_ = [("k", _vp), ("v", _vp),
+                ("k_stride_head", _i64), ("k_stride_tok", _i64),
+                ("v_stride_head", _i64), ("v_stride_tok", _i64),
+                ("k_scale", _vp), ("v_scale", _vp),
+                ("len", _i32), ("reserved", _i32)]
+
+
+class DanWorkItem(ctypes.Structure):
+    _fields_ = [("seg", _i32), ("t0", _i32), ("tq", _i32), ("ja1", _i32), ("jb0", _i32), ("jb1", _i32),
+                ("jfull", _i32), ("reserved", _i32)]
+
+
+class DanTreeAttnArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("in_dtype", _i32), ("out_dtype", _i32),
+                ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("num_tokens", _i32),
+                ("scale", _f32),
+                ("q", _vp), ("q_stride_tok", _i64), ("q_stride_head", _i64),
+                ("k", _vp), ("k_stride_tok", _i64), ("k_stride_head", _i64),
+                ("v", _vp), ("v_stride_tok", _i64), ("v_stride_head", _i64),
+                ("out", _vp), ("o_stride_tok", _i64), ("o_stride_head", _i64),
+                ("q_scale", _vp), ("k_scale", _vp), ("v_scale", _vp),
+                ("segments", _vp), ("num_segments", _i32),
+                ("pasts", _vp), ("num_pasts", _i32),
+                ("work", _vp), ("num_work", _i32),
+                ("key_lo", _vp),
+                ("tile_q", _i32), ("reserved", _i32)]
+
+
+EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_last_error", "dan_tree_attn_abi_version")
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Load the library (once) and declare its signatures. Raises RuntimeError
+    when it is missing, unloadable or speaks another ABI version."""
+    global _lib
+    with _lock:
+        if _lib is not None and path == LIB_PATH:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built; run __graft_entry__.build() (hipcc for gfx950)")
+        import torch  # noqa: F401  -- torch's HIP runtime must be loaded first (shared soname)
+
+        lib = ctypes.CDLL(path, mode=ctypes.RTLD_LOCAL)
+        lib.dan_tree_attn_fwd.argtypes = [ctypes.POINTER(DanTreeAttnArgs), _vp]
+        lib.dan_tree_attn_fwd.restype = ctypes.c_int
+        lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
+        lib.dan_tree_attn_tile_q.restype = ctypes.c_int
+        lib.dan_tree_attn_last_error.argtypes = []
+        lib.dan_tree_attn_last_error.restype = ctypes.c_char_p
+        lib.dan_tree_attn_abi_version.argtypes = []
+        lib.dan_tree_attn_abi_version.restype = ctypes.c_int
+        got = lib.dan_tree_attn_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"{path} speaks ABI {got}, this package {ABI_VERSION}; rebuild it")
+        if path == LIB_PATH:
+            _lib = lib
+        return lib
+
+
+def last_error(lib):
+    msg = lib.dan_tree_attn_last_error()
+    return msg.decode() if msg else ""
+
+
+def tile_q(num_heads, num_kv_heads, lib=None):
+    """Queries per work item the kernel expects (0: unsupported head layout)."""
+    return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads)
+
+
+def forward(args, stream, lib=None):
+    """Launch; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_tree_attn_fwd(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_tree_attn_fwd failed (status {rc}): {last_error(lib)}")

@@ -1,0 +1,246 @@
+"""Tree attention for packed, prefill-only reads -- the gfx950 drop-in for
+dan/attention.py.
+
+Many requests are packed into one flat token sequence; attention runs per
+request (a "segment"). Within a segment, tokens are a trunk (the prompt)
+followed by one contiguous branch per question. A query may see a key when
+
+    key comes first  and  (key is trunk or same branch)
+
+and a segment may start from cached keys and values of its prompt's leading
+tokens (``past``), which every query sees (dan/attention.py:1-13).
+
+Public names and meanings follow dan/attention.py: ``tree_mask`` (:54),
+``branch_rows_mask`` (:62), ``Segment`` (:72), ``Batch`` (:98),
+``to_device`` (:106), ``segment`` (:114), ``attend`` (:200),
+``repeat_heads`` (:273).
+
+``attend`` has one backend: the fused gfx950 kernel of ``dan_amd/csrc``
+(one launch, one online-softmax pass over exactly the visible key tiles). It
+replaces the reference's three varlen flash calls plus log-sum-exp merge
+(dan/attention.py:210-241) and its environment switch (:51, :175-176).
+There is no CPU or fallback path: CPU tensors, a missing library or an
+unsupported shape raise.
+"""
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _native
+from .plan import TilePlan
+
+
+def tree_mask(branch):
+    """[N, N] boolean mask (True = attend) from per-token branch ids (0 = trunk)
+    (dan/attention.py:54-59)."""
+    n = branch.shape[0]
+    idx = torch.arange(n, device=branch.device)
+    causal = idx[None, :] <= idx[:, None]
+    return causal & ((branch[None, :] == 0) | (branch[None, :] == branch[:, None]))
+
+
+def branch_rows_mask(branch, trunk):
+    """The tree mask's rows for branch tokens, [N - trunk, N]: each sees the
+    whole trunk and its own branch up to itself (dan/attention.py:62-69)."""
+    n = branch.shape[0]
+    cols = torch.arange(n, device=branch.device)
+    rows = cols[trunk:]
+    own = (branch[None, :] == branch[trunk:, None]) & (cols[None, :] <= rows[:, None])
+    return (cols[None, :] < trunk) | own
+
+
+@dataclass
+class Segment:
+    """One request of the packed batch (dan/attention.py:72-84)."""
+
+    start: int  # this request's new tokens are packed[start:end]
+    end: int
+    trunk: int = 0  # new trunk tokens: packed[start:start + trunk]
+    branches: list = field(default_factory=list)  # (start, end) of each branch in the packed sequence
+    past: dict | None = None  # layer -> (k, v) each [Hkv, past, D]
+    save: int = 0  # keep the cache entry after the first ``save`` new tokens
+    saved: dict = field(default_factory=dict)
+    past_len: int = 0
+    branch_ids: list = field(default_factory=list, repr=False)
+    device: str = "cpu"
+    _mask: torch.Tensor | None = field(default=None, repr=False)
+
+    @property
+    def mask(self):
+        """Branch rows of the tree mask with the past prepended as visible
+        columns, [n - trunk, past + n] (dan/attention.py:86-95). Metadata for
+        callers and tests; the kernel never materializes a mask."""
+        if self._mask is None:
+            m = branch_rows_mask(torch.tensor(self.branch_ids, device=self.device), self.trunk)
+            if self.past:
+                m = torch.cat([m.new_ones(m.shape[0], self.past_len), m], dim=1)
+            self._mask = m
+        return self._mask
+
+
+class Batch(list):
+    """The segments of one packed forward. Caches the tile plan every attention
+    layer shares (as dan/attention.py:98-103 caches ``layout``)."""
+
+    layout = None
+    recurrent = None
+    tile_plan = None
+
+
+def to_device(xs, device):
+    """A host list of indices as a long tensor on ``device`` (pinned,
+    non-blocking upload on the GPU; dan/attention.py:106-111)."""
+    t = torch.tensor(xs, dtype=torch.long)
+    if torch.device(device).type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
+
+
+def segment(start, branch, past=None, save=0, past_len=0, device="cpu"):
+    """A segment over new tokens with ``branch`` ids (trunk first, then each
+    branch contiguous), after ``past_len`` cached tokens
+    (dan/attention.py:114-126)."""
+    trunk = next((i for i, b in enumerate(branch) if b), len(branch))
+    spans, i = [], trunk
+    while i < len(branch):
+        j = i
+        while j < len(branch) and branch[j] == branch[i]:
+            j += 1
+        spans.append((start + i, start + j))
+        i = j
+    return Segment(start, start + len(branch), trunk, spans, past, save, past_len=past_len if past else 0,
+                   branch_ids=branch, device=device)
+
+
+def repeat_heads(x, rep):
+    """[N, H, D] -> [N, H * rep, D], each head repeated ``rep`` times in place
+    (dan/attention.py:273-279). The kernel maps query head h to kv head
+    h // rep by index arithmetic instead."""
+    if rep == 1:
+        return x
+    n, h, d = x.shape
+    return x[:, :, None].expand(n, h, rep, d).reshape(n, h * rep, d)
+
+
+_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_F16, torch.float32: _native.DTYPE_F32}
+
+
+def attend(q, k, v, segments, layer, scale=None):
+    """q: [H, N, D]; k, v: [Hkv, N, D] (rotary applied). Returns [H, N, D]
+    (dan/attention.py:200-207).
+
+    Side effect, as in the reference: a segment with ``save > 0`` keeps
+    ``saved[layer] = (k[:, start:start+save].clone(), v[...].clone())``.
+    The result is a [H, N, D] view of token-major [N, H, D] storage, so the
+    caller's ``o.transpose(0, 1).reshape(n, H * D)`` needs no copy. Rows not
+    covered by any segment are left uninitialized, as in the reference."""
+    for s in segments:
+        if s.save:
+            s.saved[layer] = (k[:, s.start:s.start + s.save].clone(), v[:, s.start:s.start + s.save].clone())
+    return _attend_fused(q, k, v, segments, layer, scale)
+
+
+def _check_inputs(q, k, v):
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q must be [H, N, D] and k, v [Hkv, N, D]")
+    h, n, d = q.shape
+    hkv = k.shape[0]
+    if k.shape != (hkv, n, d) or v.shape != (hkv, n, d):
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must be [Hkv, {n}, {d}]")
+    if hkv == 0 or h % hkv:
+        raise ValueError(f"{h} query heads is not a multiple of {hkv} kv heads")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k, v must share one of {list(_DTYPES)}; got {q.dtype}, {k.dtype}, {v.dtype}")
+    if d not in (64, 128):
+        raise ValueError(f"head_dim {d}: the gfx950 kernel is built for 64 and 128")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on one device")
+
+
+def _aligned(t):
+    """16-byte vector loads need 16-byte aligned rows with a unit-stride head_dim."""
+    es = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
+
+
+def _kernel_view(t):
+    return t if _aligned(t) else t.contiguous()
+
+
+def get_plan(segments, num_tokens, tile_q, device):
+    """The cached tile plan of this batch (built on first use)."""
+    plan = getattr(segments, "tile_plan", None)
+    if plan is None or not plan.matches(num_tokens, tile_q, device):
+        plan = TilePlan.build(segments, num_tokens, tile_q, device)
+        if isinstance(segments, Batch):
+            segments.tile_plan = plan
+    return plan
+
+
+def _past_table(plan, layer, hkv, d, dtype, device):
+    """Device table of DanPastDesc for ``layer`` (cached on the plan)."""
+    hit = plan.past_tables.get(layer)
+    if hit is not None:
+        return hit
+    n = len(plan.past_dicts)
+    descs = (_native.DanPastDesc * max(n, 1))()
+    refs = []
+    for i, past in enumerate(plan.past_dicts):
+        pk, pv = past[layer]
+        plen = pk.shape[1] if pk.dim() == 3 else -1
+        want = (hkv, plen, d)
+        if pk.dim() != 3 or tuple(pk.shape) != want or tuple(pv.shape) != want:
+            raise ValueError(f"past entry {i}, layer {layer}: k {tuple(pk.shape)}, v {tuple(pv.shape)}; want [Hkv, P, D]")
+        if pk.dtype != dtype or pv.dtype != dtype or pk.device != device or pv.device != device:
+            raise ValueError(f"past entry {i}, layer {layer}: dtype/device must match q")
+        pk, pv = _kernel_view(pk), _kernel_view(pv)
+        refs += [pk, pv]
+        descs[i].k, descs[i].v = pk.data_ptr(), pv.data_ptr()
+        descs[i].k_stride_head, descs[i].k_stride_tok = pk.stride(0), pk.stride(1)
+        descs[i].v_stride_head, descs[i].v_stride_tok = pv.stride(0), pv.stride(1)
+        descs[i].len = plen
+    for row in plan.segs:
+        if row[4] >= 0 and row[3] != descs[row[4]].len:
+            raise ValueError(f"segment past_len {row[3]} differs from its past entry's {descs[row[4]].len} keys")
+    raw = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8)
+    table = raw.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else raw
+    plan.past_tables[layer] = (table, refs)
+    return plan.past_tables[layer]
+
+
+def _attend_fused(q, k, v, segments, layer, scale):
+    if not q.is_cuda:
+        raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
+                           f"{q.device} (the masked CPU path is the test oracle, not a backend)")
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise NotImplementedError("the gfx950 tree-attention kernel is forward-only")
+    _check_inputs(q, k, v)
+    lib = _native.load()
+    h, n, d = q.shape
+    hkv = k.shape[0]
+    tile_q = _native.tile_q(h, hkv, lib)
+    if tile_q <= 0:
+        raise ValueError(f"unsupported head layout H={h}, Hkv={hkv}")
+    plan = get_plan(segments, n, tile_q, q.device)
+    table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
+    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    out = torch.empty((n, h, d), dtype=q.dtype, device=q.device)
+    if len(plan.work):
+        a = _native.DanTreeAttnArgs()
+        a.abi_version = _native.ABI_VERSION
+        a.in_dtype = a.out_dtype = _DTYPES[q.dtype]
+        a.num_heads, a.num_kv_heads, a.head_dim, a.num_tokens = h, hkv, d, n
+        a.scale = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+        a.q, a.q_stride_tok, a.q_stride_head = q.data_ptr(), q.stride(1), q.stride(0)
+        a.k, a.k_stride_tok, a.k_stride_head = k.data_ptr(), k.stride(1), k.stride(0)
+        a.v, a.v_stride_tok, a.v_stride_head = v.data_ptr(), v.stride(1), v.stride(0)
+        a.out, a.o_stride_tok, a.o_stride_head = out.data_ptr(), out.stride(0), out.stride(1)
+        a.segments, a.num_segments = plan.segs_d.data_ptr(), len(plan.segs)
+        a.pasts, a.num_pasts = table.data_ptr(), len(plan.past_dicts)
+        a.work, a.num_work = plan.work_d.data_ptr(), len(plan.work)
+        a.key_lo = plan.key_lo_d.data_ptr()
+        a.tile_q = tile_q
+        _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
+    return out.transpose(0, 1)

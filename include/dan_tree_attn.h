@@ -1,0 +1,156 @@
+/*
+ * dan_tree_attn.h -- C ABI of the gfx950 tree-masked prefill attention.
+ *
+ * One packed token sequence holds many requests ("segments"). Inside a
+ * segment the new tokens are a trunk followed by contiguous branches; a
+ * segment may start after `past_len` cached prefix tokens whose keys and
+ * values live in separate [Hkv, P, D] tensors. A query sees a key iff the key
+ * comes first and the key is past, trunk, or in the query's own branch.
+ *
+ * This header replaces, as one fused launch, the GPU leg of
+ *   dan/attention.py:200-207   attend(q, k, v, segments, layer, scale=None)
+ *   dan/attention.py:210-241   _attend_varlen: three varlen flash calls
+ *                              (trunk causal, branch-vs-trunk, branch-causal)
+ *                              plus the log-sum-exp merge of dan/fused.py:94-101
+ * and the metadata those calls consume:
+ *   dan/attention.py:72-126    Segment / segment()   -> DanSegmentDesc
+ *   dan/attention.py:138-172   ReadLayout.build      -> DanWorkItem list + key_lo
+ *   dan/cache.py:15            prefix-cache entry    -> DanPastDesc
+ *
+ * Conventions
+ *  - All tensors are device memory owned by the caller. The library borrows
+ *    the pointers for one stream-ordered launch, allocates nothing and keeps
+ *    nothing.
+ *  - Strides are in elements. The head_dim axis must have unit stride.
+ *  - Every entry point returns 0 on success; on failure it returns a nonzero
+ *    DanStatus and dan_tree_attn_last_error() describes the failure (a
+ *    thread-local string, valid until the next call on the same thread).
+ *  - The launch is asynchronous on `stream` (a hipStream_t); nothing here
+ *    synchronizes.
+ */
+#ifndef DAN_TREE_ATTN_H
+#define DAN_TREE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DAN_TREE_ATTN_ABI_VERSION 1
+
+/* Keys per key tile; the work list's key-tile indices count in these. */
+#define DAN_TREE_ATTN_KEY_TILE 64
+
+typedef enum {
+  DAN_OK = 0,
+  DAN_ERR_INVALID_ARGUMENT = 1,
+  DAN_ERR_UNSUPPORTED = 2,
+  DAN_ERR_LAUNCH = 3,
+  DAN_ERR_VERSION = 4
+} DanStatus;
+
+typedef enum {
+  DAN_DTYPE_BF16 = 0,
+  DAN_DTYPE_F16 = 1,
+  DAN_DTYPE_F32 = 2,  /* fp32 in/out; staged to bf16 for the matrix cores */
+  DAN_DTYPE_E4M3 = 3  /* OCP float8 e4m3fn inputs with per-tensor fp32 scales */
+} DanDtype;
+
+/* One request of the packed batch (dan/attention.py:72-84, :114-126).
+ * New tokens are packed rows [start, start + n): the first `trunk` are the
+ * trunk, the rest are branches (each contiguous). */
+typedef struct {
+  int32_t start;
+  int32_t n;
+  int32_t trunk;
+  int32_t past_len; /* P: cached prefix tokens before the trunk (0: none) */
+  int32_t past_idx; /* index into DanTreeAttnArgs.pasts, -1 when past_len == 0 */
+  int32_t reserved[3];
+} DanSegmentDesc;
+
+/* One prefix-cache entry for the current layer: k, v each [Hkv, len, D]
+ * (dan/cache.py:15, dan/attention.py:202-204, :254-257). Several segments may
+ * point at the same entry. k_scale / v_scale are device fp32 scalars for
+ * DAN_DTYPE_E4M3 and ignored otherwise. */
+typedef struct {
+  const void *k;
+  const void *v;
+  int64_t k_stride_head, k_stride_tok;
+  int64_t v_stride_head, v_stride_tok;
+  const float *k_scale;
+  const float *v_scale;
+  int32_t len;
+  int32_t reserved;
+} DanPastDesc;
+
+/* One query tile of one segment (replaces ReadLayout's cu_seqlens,
+ * dan/attention.py:138-172). Queries are the segment's new tokens
+ * [t0, t0 + tq) (segment-local). Keys are counted in "segment key
+ * coordinates": 0..P-1 are the past, P.. are the new tokens. The key tiles
+ * visited are [0, ja1) then [jb0, jb1) (tiles of DAN_TREE_ATTN_KEY_TILE keys;
+ * jb0 >= ja1); tiles below `jfull` are visible to every query of the tile and
+ * are not masked. */
+typedef struct {
+  int32_t seg;
+  int32_t t0;
+  int32_t tq;
+  int32_t ja1;
+  int32_t jb0;
+  int32_t jb1;
+  int32_t jfull;
+  int32_t reserved;
+} DanWorkItem;
+
+typedef struct {
+  int32_t abi_version; /* DAN_TREE_ATTN_ABI_VERSION */
+  int32_t in_dtype;    /* DanDtype of q, k, v and the pasts */
+  int32_t out_dtype;   /* DanDtype of out: bf16, f16 or f32 */
+  int32_t num_heads;   /* H */
+  int32_t num_kv_heads;/* Hkv; query head h reads kv head h / (H / Hkv) */
+  int32_t head_dim;    /* D: 64 or 128 */
+  int32_t num_tokens;  /* N packed tokens */
+  float scale;         /* softmax scale (1/sqrt(D) when the caller passes None) */
+
+  const void *q; int64_t q_stride_tok, q_stride_head; /* [N, H, D] view   */
+  const void *k; int64_t k_stride_tok, k_stride_head; /* [N, Hkv, D] view */
+  const void *v; int64_t v_stride_tok, v_stride_head; /* [N, Hkv, D] view */
+  void *out;     int64_t o_stride_tok, o_stride_head; /* [N, H, D] view   */
+
+  /* DAN_DTYPE_E4M3 only: device fp32 per-tensor scales of q, k and v. */
+  const float *q_scale;
+  const float *k_scale;
+  const float *v_scale;
+
+  const DanSegmentDesc *segments; int32_t num_segments;
+  const DanPastDesc *pasts;       int32_t num_pasts;
+  const DanWorkItem *work;        int32_t num_work;
+  /* [N] per packed token: for a branch token, P + (first new-token index of
+   * its branch); 0 for trunk tokens. Key kc is visible to query qc iff
+   *   kc <= qc  and  (kc < P + trunk  or  kc >= key_lo[query]). */
+  const int32_t *key_lo;
+  int32_t tile_q; /* queries per work item; must equal dan_tree_attn_tile_q() */
+  int32_t reserved;
+} DanTreeAttnArgs;
+
+/* Fused tree-masked attention forward: out = softmax(scale * q k^T + mask) v
+ * over every (query, visible key) pair of every segment, in one launch.
+ * Replaces dan/attention.py:200-241 (attend -> _attend_varlen) on gfx950. */
+int dan_tree_attn_fwd(const DanTreeAttnArgs *args, void *stream);
+
+/* Queries per work item the kernel expects for this head configuration
+ * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172).
+ * Returns 0 for an unsupported configuration. */
+int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char *dan_tree_attn_last_error(void);
+
+/* DAN_TREE_ATTN_ABI_VERSION of the loaded library. */
+int dan_tree_attn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DAN_TREE_ATTN_H */

@@ -1,0 +1,129 @@
+"""The C ABI without a GPU: the built library loads and exports every function
+include/dan_tree_attn.h declares, the ctypes mirror has the header's exact
+struct layout (checked by compiling the header with gcc), and argument
+errors come back as status codes with messages before any GPU call."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from dan_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dan_tree_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_native.LIB_PATH):
+        from dan_amd import _build
+
+        _build.build()
+    return _native.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dan_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_function(lib):
+    names = declared_functions()
+    assert set(names) == set(_native.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (dan_\w+)", out))
+    assert set(names) <= exported
+
+
+STRUCTS = {
+    "DanSegmentDesc": _native.DanSegmentDesc,
+    "DanPastDesc": _native.DanPastDesc,
+    "DanWorkItem": _native.DanWorkItem,
+    "DanTreeAttnArgs": _native.DanTreeAttnArgs,
+}
+
+
+def test_ctypes_layout_matches_header(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', "int main(void) {"]
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append(f'printf("ABI %d\\n", DAN_TREE_ATTN_ABI_VERSION);')
+    lines.append(f'printf("KEY_TILE %d\\n", DAN_TREE_ATTN_KEY_TILE);')
+    lines.append("return 0; }")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                               check=True).stdout.splitlines())
+    for cname, cls in STRUCTS.items():
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert int(got[f"{cname}.{fname}"]) == getattr(cls, fname).offset, f"{cname}.{fname}"
+    assert int(got["ABI"]) == _native.ABI_VERSION
+    assert int(got["KEY_TILE"]) == _native.KEY_TILE
+
+
+def test_abi_version_and_tile_q(lib):
+    assert lib.dan_tree_attn_abi_version() == _native.ABI_VERSION
+    assert _native.tile_q(32, 8, lib) == 64   # rep 4: 4 heads x 64 tokens per work group
+    assert _native.tile_q(8, 2, lib) == 64
+    assert _native.tile_q(14, 2, lib) == 64   # rep 7: two head chunks
+    assert _native.tile_q(16, 8, lib) == 128  # rep 2
+    assert _native.tile_q(8, 8, lib) == 256   # rep 1
+    assert _native.tile_q(12, 8, lib) == 0    # not a multiple
+    assert _native.tile_q(0, 8, lib) == 0
+
+
+def _args(**kw):
+    a = _native.DanTreeAttnArgs()
+    a.abi_version = _native.ABI_VERSION
+    a.in_dtype = a.out_dtype = _native.DTYPE_BF16
+    a.num_heads, a.num_kv_heads, a.head_dim, a.num_tokens = 32, 8, 128, 16
+    a.scale = 0.088
+    a.tile_q = 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=99), _native.ERR_VERSION, "abi_version"),
+    (dict(num_heads=30), _native.ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(head_dim=96), _native.ERR_UNSUPPORTED, "head_dim"),
+    (dict(tile_q=32), _native.ERR_INVALID_ARGUMENT, "tile_q"),
+    (dict(num_work=3), _native.ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(num_work=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+])
+def test_argument_errors(lib, kw, status, needle):
+    rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_null_args(lib):
+    assert lib.dan_tree_attn_fwd(None, None) == _native.ERR_INVALID_ARGUMENT
+    assert "NULL" in _native.last_error(lib)
+
+
+def test_empty_work_is_a_no_op(lib):
+    """Nothing to do: success without touching the GPU."""
+    assert lib.dan_tree_attn_fwd(ctypes.byref(_args(num_work=0)), None) == _native.OK
+    assert _native.last_error(lib) == ""
+
+
+def test_bad_scale_and_dtype(lib):
+    x = ctypes.c_int(0)
+    p = ctypes.addressof(x)
+    full = dict(num_work=1, q=p, k=p, v=p, out=p, segments=p, work=p, key_lo=p)
+    assert lib.dan_tree_attn_fwd(ctypes.byref(_args(scale=0.0, **full)), None) == _native.ERR_INVALID_ARGUMENT
+    assert "scale" in _native.last_error(lib)
+    bad = _args(in_dtype=_native.DTYPE_BF16, out_dtype=_native.DTYPE_F32, **full)
+    assert lib.dan_tree_attn_fwd(ctypes.byref(bad), None) == _native.ERR_UNSUPPORTED

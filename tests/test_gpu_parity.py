@@ -1,0 +1,213 @@
+"""Parity of the gfx950 kernel (through dan_amd.attend -> C ABI) with the CPU
+oracle on identical seeded inputs.
+
+Bars: bf16/fp16/fp32 outputs within max-abs 2e-2 of the fp32 oracle; the
+label-softmax readout (rms_norm of the read row, seeded label heads,
+softmax) within 1e-3 in probability."""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from dan_amd import workloads as W
+from dan_amd.attention import Batch, attend, segment
+from oracle import tree_attention as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+READOUT_ATOL = 1e-3
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def check(w, name, atol=ATOL, readout=True):
+    say(f"{name}: N={w.num_tokens} H={w.q.shape[0]} Hkv={w.k.shape[0]} D={w.q.shape[2]} {w.q.dtype} "
+        f"segments={len(w.segments)}")
+    out = attend(w.q, w.k, w.v, w.segments, w.layer)
+    torch.cuda.synchronize()
+    assert out.shape == w.q.shape and out.dtype == w.q.dtype
+    ref = O.attend_dense(w.q, w.k, w.v, w.segments, w.layer)
+    got = out.float().cpu()
+    rows = torch.cat([torch.arange(s.start, s.end) for s in w.segments])
+    err = (got[:, rows] - ref[:, rows]).abs().max().item()
+    assert math.isfinite(err) and err <= atol, f"{name}: max-abs {err:.3e} > {atol}"
+    dp = 0.0
+    if readout and any(s.branches for s in w.segments):
+        nb = sum(len(s.branches) for s in w.segments)
+        wts = O.readout_weights(nb, w.q.shape[0] * w.q.shape[2], seed=11)
+        pg = O.readout_probs(out, w.segments, wts)
+        pc = O.readout_probs(ref, w.segments, wts)
+        dp = max(abs(a - b) for x, y in zip(pg, pc) for a, b in zip(x, y))
+        assert dp <= READOUT_ATOL, f"{name}: readout |dp| {dp:.2e} > {READOUT_ATOL}"
+    say(f"{name}: max-abs {err:.3e}, readout dp {dp:.2e}")
+    return out, ref
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c4"])
+def test_config_seed0(gpu, cfg):
+    check(W.CONFIGS[cfg](0, device=gpu), f"{cfg} seed 0")
+
+
+@pytest.mark.parametrize("cfg,seed", [("c2", 1), ("c2", 2), ("c3", 1), ("c3", 2), ("c1", 3)])
+def test_config_more_seeds(gpu, cfg, seed):
+    check(W.CONFIGS[cfg](seed, device=gpu), f"{cfg} seed {seed}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_reference_differential_shapes(gpu, dtype, head_dim):
+    """tests/test_runner.py:44-68 of the reference: h=8, hkv=2, mixed trees with
+    per-segment pasts, bf16 and fp16."""
+    check(W.runner_shapes(0, device=gpu, dtype=dtype, head_dim=head_dim), f"runner shapes {dtype} D={head_dim}")
+
+
+def random_batch(rng, h, hkv, d, dtype, device, max_segments=5, long=False):
+    structure, pasts = [], []
+    for _ in range(int(rng.integers(1, max_segments + 1))):
+        trunk = int(rng.integers(0, 700 if long else 150))
+        lens = [int(x) for x in rng.integers(1, 100, int(rng.integers(0, 7)))]
+        if trunk + sum(lens) == 0:
+            trunk = 1
+        structure.append((trunk, lens))
+        pasts.append(int(rng.integers(1, 300)) if rng.random() < 0.4 else 0)
+    return W.build("random", structure, h, hkv, d, dtype, device, rng, std=0.7, per_segment_past=pasts)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_trees(gpu, seed):
+    """Empty trunks, single-token branches, segments without branches,
+    per-segment pasts, ragged tiles."""
+    rng = np.random.default_rng(100 + seed)
+    d = 128 if seed % 3 else 64
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    check(random_batch(rng, 8, 2, d, dtype, gpu, long=seed % 4 == 0), f"random tree seed {seed}")
+
+
+@pytest.mark.parametrize("h,hkv", [(4, 4), (8, 4), (14, 2), (16, 2), (12, 3)])
+def test_head_layouts(gpu, h, hkv):
+    """rep = 1, 2, 7 (two head chunks, one idle wave), 8 (two chunks), 4 with 3 kv heads."""
+    rng = np.random.default_rng(h * 31 + hkv)
+    check(random_batch(rng, h, hkv, 128, torch.bfloat16, gpu), f"heads {h}/{hkv}")
+
+
+def test_single_tokens_and_tiny_segments(gpu):
+    rng = np.random.default_rng(5)
+    structure = [(1, []), (0, [1]), (1, [1, 1, 1]), (0, [2, 3]), (65, [1]), (64, [64])]
+    w = W.build("tiny", structure, 8, 2, 128, torch.bfloat16, gpu, rng, per_segment_past=[0, 3, 0, 70, 64, 1])
+    check(w, "tiny segments")
+
+
+def test_fp32_config1_layout(gpu):
+    """fp32 in, fp32 out (staged to bf16 for the matrix cores)."""
+    out, _ = check(W.config1(1, device=gpu), "c1 seed 1")
+    assert out.dtype == torch.float32
+
+
+def test_output_is_token_major_view(gpu):
+    w = W.config2(0, device=gpu)
+    say("output layout")
+    out = attend(w.q, w.k, w.v, w.segments, 0)
+    h, n, d = w.q.shape
+    assert out.shape == (h, n, d) and out.stride() == (d, h * d, 1)
+    flat = out.transpose(0, 1).reshape(n, h * d)  # the o_proj input of dan/models/llama.py:87
+    assert flat.data_ptr() == out.data_ptr()
+
+
+def test_deterministic(gpu):
+    w = W.config3(0, device=gpu)
+    say("determinism c3")
+    a = attend(w.q, w.k, w.v, w.segments, 0)
+    b = attend(w.q, w.k, w.v, w.segments, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_save_side_effect(gpu):
+    """dan/attention.py:202-204: saved[layer] holds clones of the first `save` keys/values."""
+    w = W.config2(0, device=gpu)
+    w.segments[1].save = 50
+    say("save side effect")
+    attend(w.q, w.k, w.v, w.segments, 3)
+    s = w.segments[1]
+    sk, sv = s.saved[3]
+    assert torch.equal(sk, w.k[:, s.start:s.start + 50]) and torch.equal(sv, w.v[:, s.start:s.start + 50])
+    assert sk.data_ptr() != w.k.data_ptr() and sk.is_contiguous()
+
+
+def test_misaligned_and_contiguous_inputs(gpu):
+    """Views whose rows are not 16-byte aligned take a contiguous copy; fully
+    contiguous [H, N, D] inputs work as they are."""
+    w = W.config2(1, device=gpu)
+    ref = attend(w.q, w.k, w.v, w.segments, 0).float()
+    say("misaligned views")
+    big = torch.empty(w.q.numel() + 1, dtype=w.q.dtype, device=gpu)
+    q_odd = big[1:].view(w.q.shape).copy_(w.q)  # base 2 bytes off
+    got = attend(q_odd, w.k.contiguous(), w.v.contiguous(), w.segments, 0).float()
+    torch.cuda.synchronize()
+    assert (got - ref).abs().max().item() == 0.0
+
+
+def test_side_stream(gpu):
+    """The launch goes to the caller's current stream."""
+    w = W.config2(2, device=gpu)
+    say("side stream")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out = attend(w.q, w.k, w.v, w.segments, 0)
+    s.synchronize()
+    ref = attend(w.q, w.k, w.v, w.segments, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_plan_is_cached_on_batch(gpu):
+    w = W.config2(0, device=gpu)
+    say("plan cache")
+    attend(w.q, w.k, w.v, w.segments, 0)
+    plan = w.segments.tile_plan
+    attend(w.q, w.k, w.v, w.segments, 0)
+    assert w.segments.tile_plan is plan
+    assert 0 in plan.past_tables
+
+
+def test_errors_are_python_exceptions(gpu):
+    w = W.config2(0, device=gpu)
+    say("error paths")
+    with pytest.raises(NotImplementedError):
+        with torch.enable_grad():
+            attend(w.q.detach().requires_grad_(), w.k, w.v, w.segments, 0)
+    with pytest.raises(ValueError):
+        attend(w.q, w.k[:, :10], w.v[:, :10], w.segments, 0)
+    bad = Batch([segment(0, [0] * 10 + [1] * 5)])
+    bad[0].end = w.num_tokens + 5
+    with pytest.raises(ValueError):
+        attend(w.q, w.k, w.v, bad, 0)
+
+
+def test_full_size_invariants(gpu):
+    """At the 8192-token budget: outputs are convex combinations of visible
+    values (|o| <= max |v| per head group), and permuting whole segments of the
+    packed batch permutes the output rows exactly."""
+    w = W.config3(0, device=gpu)
+    say("full-size invariants c3")
+    out = attend(w.q, w.k, w.v, w.segments, 0).float()
+    vmax = max(w.v.float().abs().max().item(), w.segments[0].past[0][1].float().abs().max().item())
+    assert out.abs().max().item() <= vmax * (1 + 2 ** -7)
+    order = list(range(len(w.segments)))[::-1]
+    rows, segs, start = [], Batch(), 0
+    for i in order:
+        s = w.segments[i]
+        rows += range(s.start, s.end)
+        segs.append(segment(start, s.branch_ids, s.past, 0, s.past_len, str(gpu)))
+        start += s.end - s.start
+    rows = torch.tensor(rows, device=gpu)
+    got = attend(w.q[:, rows], w.k[:, rows], w.v[:, rows], segs, 0).float()
+    torch.cuda.synchronize()
+    assert torch.equal(got, out[:, rows])
