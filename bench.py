@@ -88,6 +88,18 @@ def cpu_baseline(name, seed, flops, n_tokens):
             "seconds": round(t, 4), "tokens_per_s": round(n_tokens / t, 1)}
 
 
+def copy_calibration(mib, steps):
+    """A plain copy of known size: FETCH_SIZE and WRITE_SIZE of its dispatches
+    give the counters' scale (read bytes = written bytes = mib MiB each)."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "copies": steps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,6 +108,9 @@ def main():
     ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead of attention, run --steps plain device copies of this many MiB (the calibration "
+                         "kernel for the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the tree-attention path runs on a single device "
@@ -104,6 +119,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_mib:
+        copy_calibration(args.copy_mib, args.steps)
+        return
 
     from dan_amd import _native, workloads
     from dan_amd.attention import attend

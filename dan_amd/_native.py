@@ -44,7 +44,7 @@ class DanPastDesc(ctypes.Structure):
 
 class DanWorkItem(ctypes.Structure):
     _fields_ = [("seg", _i32), ("t0", _i32), ("tq", _i32), ("ja1", _i32), ("jb0", _i32), ("jb1", _i32),
-                ("jfull", _i32), ("reserved", _i32)]
+                ("jfull", _i32), ("lo_max", _i32)]
 
 
 class DanTreeAttnArgs(ctypes.Structure):

@@ -166,7 +166,11 @@ def _aligned(t):
 
 
 def _kernel_view(t):
-    return t if _aligned(t) else t.contiguous()
+    """The tensor itself when the kernel can read it in place, else a
+    contiguous copy (unaligned rows, or token strides too large for the
+    kernel's 32-bit in-tile offsets)."""
+    small = abs(t.stride(-2)) * 64 < 2 ** 31
+    return t if _aligned(t) and small else t.contiguous()
 
 
 def get_plan(segments, num_tokens, tile_q, device):

@@ -87,13 +87,15 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
             top = p + t0 + tq  # one past the last query's own key
             kfull = min(p + t0 + 1, pt)
             ja1 = _ceil_div(min(pt, top), key_tile)
+            lo_max = 0
             if t0 + tq > t:  # the tile holds branch queries
                 first = s.start + max(t0, t)
                 jb0 = max(int(key_lo[first]) // key_tile, ja1)
                 jb1 = max(_ceil_div(top, key_tile), jb0)
+                lo_max = int(key_lo[s.start + t0 + tq - 1])  # key_lo grows along the branch region
             else:
                 jb0 = jb1 = ja1
-            items.append((i, t0, tq, ja1, jb0, jb1, kfull // key_tile, 0))
+            items.append((i, t0, tq, ja1, jb0, jb1, kfull // key_tile, lo_max))
     work = np.array(items, np.int32).reshape(-1, 8)
     cost = (work[:, 3].astype(np.int64) + work[:, 5] - work[:, 4]) if len(work) else np.zeros(0, np.int64)
     order = np.argsort(-cost, kind="stable")

@@ -53,7 +53,7 @@ typedef enum {
 typedef enum {
   DAN_DTYPE_BF16 = 0,
   DAN_DTYPE_F16 = 1,
-  DAN_DTYPE_F32 = 2,  /* fp32 in/out; staged to bf16 for the matrix cores */
+  DAN_DTYPE_F32 = 2,  /* fp32 in/out; staged to fp16 for the matrix cores */
   DAN_DTYPE_E4M3 = 3  /* OCP float8 e4m3fn inputs with per-tensor fp32 scales */
 } DanDtype;
 
@@ -90,7 +90,10 @@ typedef struct {
  * coordinates": 0..P-1 are the past, P.. are the new tokens. The key tiles
  * visited are [0, ja1) then [jb0, jb1) (tiles of DAN_TREE_ATTN_KEY_TILE keys;
  * jb0 >= ja1); tiles below `jfull` are visible to every query of the tile and
- * are not masked. */
+ * are not masked. `lo_max` is the largest key_lo of the item's queries: keys
+ * in [P + trunk, lo_max) are hidden from some of its branch queries, so only
+ * tiles meeting that range need the sibling-branch test; elsewhere the mask
+ * is causal only. */
 typedef struct {
   int32_t seg;
   int32_t t0;
@@ -99,7 +102,7 @@ typedef struct {
   int32_t jb0;
   int32_t jb1;
   int32_t jfull;
-  int32_t reserved;
+  int32_t lo_max;
 } DanWorkItem;
 
 typedef struct {

@@ -222,16 +222,18 @@ def read_rows(segments):
 
 def readout_probs(out, segments, weights, eps=1e-6):
     """Label probabilities per branch from attention output ``out`` [H, N, D]
-    (any dtype): h = rms_norm(o_row.flatten()) with weight 1 in the output's
-    dtype (as llama.py:161 normalizes), logits = W_b h in fp32
-    (llama.py:163-165), probabilities by ``label_softmax``."""
+    (any dtype): the read row's values as given, h = its RMS normalization
+    with weight 1 computed in fp32 (the normalize step of dan/fused.py:35-40,
+    as llama.py:161 applies it; the result is kept in fp32 instead of being
+    re-rounded to the activation dtype, which would make the comparison a
+    function of rounding noise), logits = W_b h in fp32 (llama.py:163-165),
+    probabilities by ``label_softmax``."""
     rows = read_rows(segments)
     probs = []
     for w, r in zip(weights, rows):
-        x = out[:, r].detach().to("cpu").reshape(-1)
-        h = rms_norm(x, torch.ones((), dtype=x.dtype), eps)
-        logits = (w.float() @ h.float()).tolist()
-        probs.append(label_softmax(logits))
+        y = out[:, r].detach().to("cpu").reshape(-1).float()
+        h = y * torch.rsqrt(y.pow(2).mean() + eps)
+        probs.append(label_softmax((w.float() @ h).tolist()))
     return probs
 
 

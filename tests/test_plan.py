@@ -35,8 +35,15 @@ def check_plan(segments, num_tokens, tile_q):
             if j < jfull:
                 assert block.shape[1] == KEY_TILE and block.all(), f"tile {j} below jfull is not fully visible"
         assert max(tiles, default=-1) < _ceil(nkeys, KEY_TILE)
-        # the kernel's per-element rule reproduces the mask inside visited tiles
+        # outside [P + trunk, lo_max) the causal rule alone is the mask
         pt = p + s.trunk
+        lo_max = int(item[7])
+        for j in tiles:
+            if j >= jfull and not (j * KEY_TILE + KEY_TILE > pt and j * KEY_TILE < lo_max):
+                keys = np.arange(j * KEY_TILE, min((j + 1) * KEY_TILE, nkeys))
+                causal = keys[None, :] <= (p + t0 + np.arange(tq))[:, None]
+                assert (causal == vis[:, keys]).all(), f"tile {j} needs the branch test but lo_max={lo_max}"
+        # the kernel's per-element rule reproduces the mask inside visited tiles
         for i in range(tq):
             qk = p + t0 + i
             lo = key_lo[s.start + t0 + i]
