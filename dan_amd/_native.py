@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 KEY_TILE = 64
 
 # DanStatus
@@ -31,7 +31,7 @@ _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c
 
 class DanSegmentDesc(ctypes.Structure):
     _fields_ = [("start", _i32), ("n", _i32), ("trunk", _i32), ("past_len", _i32), ("past_idx", _i32),
-                ("reserved", _i32 * 3)]
+                ("vt_col", _i32), ("reserved", _i32 * 2)]
 
 
 class DanPastDesc(ctypes.Structure):
@@ -48,7 +48,7 @@ class DanWorkItem(ctypes.Structure):
 
 
 class DanTreeAttnArgs(ctypes.Structure):
-    _fields_ = [("abi_version", _i32), ("in_dtype", _i32), ("out_dtype", _i32),
+    _fields_ = [("abi_version", _i32), ("in_dtype", _i32), ("out_dtype", _i32), ("v_dtype", _i32),
                 ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("num_tokens", _i32),
                 ("scale", _f32),
                 ("q", _vp), ("q_stride_tok", _i64), ("q_stride_head", _i64),
@@ -60,10 +60,13 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("pasts", _vp), ("num_pasts", _i32),
                 ("work", _vp), ("num_work", _i32),
                 ("key_lo", _vp),
-                ("tile_q", _i32), ("reserved", _i32)]
+                ("tile_q", _i32), ("vt_cols", _i32),
+                ("col_seg", _vp),
+                ("workspace", _vp), ("workspace_bytes", _i64)]
 
 
-EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_last_error", "dan_tree_attn_abi_version")
+EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_workspace_size", "dan_tree_attn_last_error",
+           "dan_tree_attn_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -85,6 +88,8 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_fwd.restype = ctypes.c_int
         lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
         lib.dan_tree_attn_tile_q.restype = ctypes.c_int
+        lib.dan_tree_attn_workspace_size.argtypes = [_i32, _i32, _i32]
+        lib.dan_tree_attn_workspace_size.restype = _i64
         lib.dan_tree_attn_last_error.argtypes = []
         lib.dan_tree_attn_last_error.restype = ctypes.c_char_p
         lib.dan_tree_attn_abi_version.argtypes = []
@@ -105,6 +110,11 @@ def last_error(lib):
 def tile_q(num_heads, num_kv_heads, lib=None):
     """Queries per work item the kernel expects (0: unsupported head layout)."""
     return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads)
+
+
+def workspace_size(num_kv_heads, head_dim, vt_cols, lib=None):
+    """Bytes of device workspace one launch needs (0: invalid arguments)."""
+    return (lib or load()).dan_tree_attn_workspace_size(num_kv_heads, head_dim, vt_cols)
 
 
 def forward(args, stream, lib=None):

@@ -183,6 +183,11 @@ def get_plan(segments, num_tokens, tile_q, device):
     return plan
 
 
+def _qk_dtype(dtype):
+    """Matrix-core type of q and k: fp32 models stage them as fp16 (|x| < 65504)."""
+    return torch.float16 if dtype == torch.float32 else dtype
+
+
 def _past_table(plan, layer, hkv, d, dtype, device):
     """Device table of DanPastDesc for ``layer`` (cached on the plan)."""
     hit = plan.past_tables.get(layer)
@@ -199,7 +204,7 @@ def _past_table(plan, layer, hkv, d, dtype, device):
             raise ValueError(f"past entry {i}, layer {layer}: k {tuple(pk.shape)}, v {tuple(pv.shape)}; want [Hkv, P, D]")
         if pk.dtype != dtype or pv.dtype != dtype or pk.device != device or pv.device != device:
             raise ValueError(f"past entry {i}, layer {layer}: dtype/device must match q")
-        pk, pv = _kernel_view(pk), _kernel_view(pv)
+        pk, pv = _kernel_view(pk.to(_qk_dtype(dtype))), _kernel_view(pv)
         refs += [pk, pv]
         descs[i].k, descs[i].v = pk.data_ptr(), pv.data_ptr()
         descs[i].k_stride_head, descs[i].k_stride_tok = pk.stride(0), pk.stride(1)
@@ -214,6 +219,15 @@ def _past_table(plan, layer, hkv, d, dtype, device):
     return plan.past_tables[layer]
 
 
+def _workspace(plan, nbytes, device):
+    """Device scratch for the kernel's fp16 V^T copy, cached on the plan and
+    reused by every layer (launches are ordered on the stream)."""
+    ws = plan.workspace.get(nbytes)
+    if ws is None:
+        ws = plan.workspace[nbytes] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return ws
+
+
 def _attend_fused(q, k, v, segments, layer, scale):
     if not q.is_cuda:
         raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
@@ -221,6 +235,8 @@ def _attend_fused(q, k, v, segments, layer, scale):
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         raise NotImplementedError("the gfx950 tree-attention kernel is forward-only")
     _check_inputs(q, k, v)
+    if scale is not None and not (float(scale) > 0 and math.isfinite(float(scale))):
+        raise ValueError(f"scale {scale}: the kernel needs a finite positive softmax scale")
     lib = _native.load()
     h, n, d = q.shape
     hkv = k.shape[0]
@@ -229,12 +245,18 @@ def _attend_fused(q, k, v, segments, layer, scale):
         raise ValueError(f"unsupported head layout H={h}, Hkv={hkv}")
     plan = get_plan(segments, n, tile_q, q.device)
     table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
-    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
-    out = torch.empty((n, h, d), dtype=q.dtype, device=q.device)
+    out_dtype = q.dtype
+    qk_dtype = _qk_dtype(q.dtype)
+    q, k, v = _kernel_view(q.to(qk_dtype)), _kernel_view(k.to(qk_dtype)), _kernel_view(v)
+    out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
     if len(plan.work):
+        nbytes = _native.workspace_size(hkv, d, plan.vt_cols, lib)
+        ws = _workspace(plan, nbytes, q.device)
         a = _native.DanTreeAttnArgs()
         a.abi_version = _native.ABI_VERSION
-        a.in_dtype = a.out_dtype = _DTYPES[q.dtype]
+        a.in_dtype = _DTYPES[qk_dtype]
+        a.v_dtype = _DTYPES[v.dtype]
+        a.out_dtype = _DTYPES[out_dtype]
         a.num_heads, a.num_kv_heads, a.head_dim, a.num_tokens = h, hkv, d, n
         a.scale = (1.0 / math.sqrt(d)) if scale is None else float(scale)
         a.q, a.q_stride_tok, a.q_stride_head = q.data_ptr(), q.stride(1), q.stride(0)
@@ -246,5 +268,8 @@ def _attend_fused(q, k, v, segments, layer, scale):
         a.work, a.num_work = plan.work_d.data_ptr(), len(plan.work)
         a.key_lo = plan.key_lo_d.data_ptr()
         a.tile_q = tile_q
+        a.vt_cols = plan.vt_cols
+        a.col_seg = plan.col_seg_d.data_ptr()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

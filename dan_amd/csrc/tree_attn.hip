@@ -1,37 +1,47 @@
 // Fused tree-masked prefill attention for gfx950 (MI355X, CDNA4).
 //
-// One launch computes, for every segment of a packed batch, what
-// dan/attention.py:210-241 computes with three varlen flash calls, six gathers
-// and a log-sum-exp merge: trunk queries attend causally over [past; trunk],
-// branch queries attend to [past; trunk] and causally to their own branch.
-// Here every (query tile, kv head) work group walks only the key tiles its
-// queries can see, in one online-softmax pass, so there is no merge.
+// One dan_tree_attn_fwd call computes, for every segment of a packed batch,
+// what dan/attention.py:210-241 computes with three varlen flash calls, six
+// gathers and a log-sum-exp merge: trunk queries attend causally over
+// [past; trunk], branch queries attend to [past; trunk] and causally to their
+// own branch. Each (query tile, kv head) work group walks only the key tiles
+// its queries can see, in one online-softmax pass, so there is no merge.
 //
-// Work decomposition
-//   - A work group (4 waves of 64 lanes) owns one work item (a tile of query
-//     tokens of one segment) for one kv head. With rep = H / Hkv query heads
-//     per kv head, wave w takes query head (w % hpw) of the kv group and the
-//     (w / hpw)-th run of 64 tokens of the tile, so the K/V tiles staged in LDS
-//     serve every query head that shares them (GQA head packing).
+// Two kernels run on the caller's stream:
+//   vt_pack_kernel     V (and each prefix-cache entry's v) -> fp16 V^T in the
+//                      caller's workspace, [Hkv][D][columns], one 64-aligned
+//                      column range per segment holding [past; new] keys.
+//   tree_attn_kernel   the attention itself.
+//
+// Work decomposition of tree_attn_kernel
+//   - A work group (8 waves, 2 per SIMD) owns one work item (a tile of query
+//     tokens of one segment) for one kv head. Wave w takes query head
+//     (w % hpw) of the kv group and the (w / hpw)-th run of 32 tokens, so the
+//     K / V^T tiles staged in LDS serve every query head that shares them
+//     (GQA head packing).
 //   - blockIdx.x = item * (Hkv * chunks) + kv head + Hkv * chunk: consecutive
 //     blocks land on different XCDs, so with Hkv = 8 each XCD's L2 holds one
 //     kv head's keys and values.
 //
-// Per wave, per key tile of 64 keys (bf16 / fp16 matrix cores):
-//   S^T[key, query] = K Q^T      v_mfma_f32_32x32x16: A = K rows from LDS,
-//                                B = Q held in registers. Queries sit on the
-//                                lanes, so each lane owns its query's softmax
-//                                state and the row max/sum need one cross-half
-//                                exchange only.
+// Per wave and key tile of 64 keys:
+//   S^T[key, query] = K Q^T      v_mfma_f32_32x32x16 (bf16 or fp16): A = K rows
+//                                from LDS, B = Q held in registers. Queries sit
+//                                on the lanes, so each lane owns its query's
+//                                softmax state; row max/sum need one cross-half
+//                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max is raised lazily (only when it grows by more than kLazyRescale) so the
-//   O accumulators are rarely rescaled.
-//   O^T[d, query] += V^T P^T     A = V^T rows from LDS (V is transposed while
-//                                it is staged), B = P^T straight from the S^T
-//                                registers: K rows are staged in a permuted
-//                                order so that the S^T accumulator layout is
-//                                already the B-operand layout of P^T.
-// K and V tiles are double-buffered in LDS in padded rows (no bank conflicts).
+//   max is raised lazily (only when it grows by more than kLazyRescale), so
+//   the O accumulators are rarely rescaled.
+//   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
+//                                B = P^T straight from the S^T registers: K rows
+//                                are staged in a permuted order that makes the
+//                                S^T accumulator layout the B-operand layout.
+// Staging: K and V^T tiles go from global memory straight into LDS
+// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep, into
+// rows padded by 16 bytes (conflict-free operand reads at constant offsets).
+// Pipelining: while the softmax of tile j runs on the VALU, the wave already
+// issues S = K Q^T of tile j+1 on the matrix core; the tile two ahead is in
+// flight from memory.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -40,10 +50,6 @@
 #include <stdio.h>
 
 #include "dan_tree_attn.h"
-
-#ifndef DAN_TREE_ATTN_SKEW
-#define DAN_TREE_ATTN_SKEW 1
-#endif
 
 namespace dan {
 
@@ -66,15 +72,26 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr f16x2 kOnes2 = {(_Float16)1.0f, (_Float16)1.0f};
 
 struct KParams {
-  const void *q, *k, *v;
+  const void *q, *k;
   void *o;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+  const _Float16 *vt;
+  int64_t q_st, q_sh, k_st, k_sh, o_st, o_sh;
   const DanSegmentDesc *segs;
   const DanPastDesc *pasts;
   const DanWorkItem *work;
   const int32_t *key_lo;
-  int32_t num_kv_heads, rep, hpw, chunks;
+  int32_t num_kv_heads, rep, hpw, chunks, vt_cols;
   float c;  // softmax scale * log2(e)
+};
+
+struct PackParams {
+  const void *v;
+  int64_t v_st, v_sh;
+  const DanSegmentDesc *segs;
+  const DanPastDesc *pasts;
+  const int32_t *col_seg;
+  _Float16 *vt;
+  int32_t num_kv_heads, vt_cols;
 };
 
 // ---------------------------------------------------------------- element I/O
@@ -187,52 +204,114 @@ __device__ inline uint32_t half_of(u32x4 v, int e) {
 // of its 32-key block -- exactly the k-order of the P^T B operand.
 __device__ inline int k_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
-// LDS layout: two K buffers (rows [64][D]) and three V^T buffers (rows
-// [D][64]); three V buffers let the second wave group run one phase behind
-// the first (see the kernel). Rows are padded by 16 bytes so the 32 rows one
-// MFMA operand read touches fall in distinct banks, and every read of a wave
-// is one base address plus a compile-time offset.
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone).
+template <int N>
+__device__ inline void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Work-group barrier without the memory fence __syncthreads() adds: the fence
+// makes the compiler drain every outstanding direct load (vmcnt(0)), while a
+// stage buffer only needs its own loads counted down (wait_vmem) before the
+// barrier. LDS reads are drained so no wave still reads a buffer that the next
+// loads overwrite; the "memory" clobber keeps the compiler from moving memory
+// accesses across the barrier.
+__device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+#define DAN_LDS __attribute__((address_space(3)))
+// One 16-byte direct load per lane into LDS: lane l writes lds + 16 * l.
+template <typename T>
+__device__ inline void load_to_lds(const T *src, uint8_t *lds) {
+  __builtin_amdgcn_global_load_lds((const DAN_GLOBAL void *)src, (DAN_LDS void *)lds, 16, 0, 0);
+}
+
+// LDS layout of one of four stage buffers: K rows [64][D] (row m holds key
+// k_row(m)) then V^T rows [D][64], every row padded by one 16-byte chunk. A
+// buffer is a whole number of 1 KB direct-load blocks (K: 64 * (D/8 + 1)
+// chunks, V^T: D * 9 chunks); the pad chunks receive a duplicate of the row's
+// last chunk. A 1 KB sink after the buffers absorbs the direct-load slots that
+// round the per-wave load count up to a constant.
 template <int D>
-struct LdsLayout {
-  static constexpr int kRow = D * 2 + 16;
-  static constexpr int vRow = kKeyTile * 2 + 16;
+struct Lds {
+  static constexpr int kChunks = D / 8 + 1;
+  static constexpr int kRow = kChunks * 16;
   static constexpr int kBytes = kKeyTile * kRow;
+  static constexpr int kInsts = kKeyTile * kChunks / 64;
+  static constexpr int vChunks = kKeyTile / 8 + 1;
+  static constexpr int vRow = vChunks * 16;
   static constexpr int vBytes = D * vRow;
-  static constexpr int kBase = 0;
-  static constexpr int vBase = 2 * kBytes;
-  static constexpr int total = 2 * kBytes + 3 * vBytes;
+  static constexpr int vInsts = D * vChunks / 64;
+  static constexpr int slots = (kInsts + vInsts + kWaves - 1) / kWaves;  // direct loads per wave per tile
+  static constexpr int buf = kBytes + vBytes;
+  static constexpr int nbuf = 4;
+  static constexpr int sink = nbuf * buf;
+  static constexpr int total = sink + 1024;
+  static_assert(kBytes == kInsts * 1024 && vBytes == vInsts * 1024, "whole 1 KB blocks");
 };
 
-// ---------------------------------------------------------------- kernel
-// TIn: q/k/v element type. TQK: matrix-core type of S = K Q^T (bf16 for bf16
-// inputs, fp16 otherwise). P V always runs in fp16: P in [0, 2^8] keeps 11
-// significant bits instead of bf16's 8, and bf16 V converts to fp16 exactly
-// inside fp16's range.
-// kSkew: the second wave group (waves 4-7, one per SIMD next to a wave of the
-// first group) runs each iteration as [P V of the previous tile, S = K Q^T,
-// softmax] while the first runs [S, softmax, P V], so on every SIMD one wave
-// feeds the matrix core while the other runs its softmax.
-template <typename TIn, typename TOut, typename TQK, int D, bool kSkew>
+// ---------------------------------------------------------------- V^T packing
+// One work group per (64-column block of the V^T copy, kv head): reads the 64
+// keys of the block (past rows from the segment's prefix-cache entry, new rows
+// from v; zero past the segment's end), converts them to fp16 and writes them
+// transposed, 128 contiguous bytes per d.
+template <typename TV, int D>
+__global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
+  constexpr int CPR = D / 8;
+  constexpr int KPP = 256 / CPR;  // keys per load pass
+  __shared__ __attribute__((aligned(16))) uint16_t tile[D][kKeyTile + 8];
+  const int kvh = blockIdx.x % p.num_kv_heads, cb = blockIdx.x / p.num_kv_heads;
+  const DanSegmentDesc sg = load_entry(p.segs + *gbl(p.col_seg + cb));
+  const int key0 = cb * kKeyTile - sg.vt_col;
+  const int P = sg.past_len, PN = P + sg.n;
+  const TV *vp = static_cast<const TV *>(p.v) + (int64_t)kvh * p.v_sh;
+  const TV *pvp = nullptr;
+  int64_t pv_st = 0;
+  if (P > 0) {
+    const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
+    pvp = static_cast<const TV *>(pd.v) + (int64_t)kvh * pd.v_stride_head;
+    pv_st = pd.v_stride_tok;
+  }
+  const int c = threadIdx.x % CPR;
+#pragma unroll
+  for (int pass = 0; pass < kKeyTile / KPP; ++pass) {
+    const int kr = pass * KPP + threadIdx.x / CPR;
+    const int key = key0 + kr;
+    u32x4 x = {0, 0, 0, 0};
+    if (key < PN)
+      x = load8<TV, _Float16>(key < P ? pvp + (int64_t)key * pv_st + 8 * c
+                                      : vp + (int64_t)(sg.start + key - P) * p.v_st + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[8 * c + e][kr] = (uint16_t)half_of(x, e);
+  }
+  __syncthreads();
+  _Float16 *dst = p.vt + (int64_t)kvh * D * p.vt_cols + (int64_t)cb * kKeyTile;
+  for (int i = threadIdx.x; i < D * 8; i += 256) {
+    const int d = i >> 3, ch = i & 7;
+    *gbl_mut(reinterpret_cast<u32x4 *>(dst + (int64_t)d * p.vt_cols + 8 * ch)) =
+        *reinterpret_cast<const u32x4 *>(&tile[d][8 * ch]);
+  }
+}
+
+// ---------------------------------------------------------------- attention
+// TQK: matrix-core type of S = K Q^T (q, k and the pasts' k). P V always runs
+// in fp16: P in [0, 2^8] keeps 11 significant bits instead of bf16's 8, and
+// the V^T copy is fp16.
+template <typename TQK, typename TOut, int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
-void tree_attn_fwd_kernel(const KParams p) {
-  using TPV = _Float16;
-  constexpr int CPR = D / 8;                      // 16-byte chunks per K row
-  constexpr int ROWS_PER_PASS = kThreads / CPR;   // K rows one pass loads
-  constexpr int KCH = kKeyTile / ROWS_PER_PASS;   // passes (= V keys per thread)
-  constexpr int ND = D / 32;                      // 32-row d blocks of O^T
-  constexpr int NK = D / 16;                      // k-steps of Q K^T
-  constexpr int NKG = kKeyTile / KCH;             // V key groups of KCH keys
-  constexpr int KROW = LdsLayout<D>::kRow;
-  constexpr int VROW = LdsLayout<D>::vRow;
-  constexpr int KBYTES = LdsLayout<D>::kBytes;
-  constexpr int VBYTES = LdsLayout<D>::vBytes;
-  constexpr int VBASE = LdsLayout<D>::vBase;
-  static_assert(KCH == 1 || KCH == 2, "head_dim must be 64 or 128");
+void tree_attn_kernel(const KParams p) {
+  using L = Lds<D>;
+  constexpr int NK = D / 16;   // k-steps of Q K^T
+  constexpr int ND = D / 32;   // 32-row d blocks of O^T
+  constexpr int SLOTS = L::slots;
+  constexpr int KC = L::kChunks;
+  constexpr int VC = L::vChunks;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, hl = lane >> 5, lq = lane & 31;
-  const bool lagging = kSkew && wave >= kWaves / 2;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, hl = lane >> 5, lq = lane & 31;
 
   const int groups = p.num_kv_heads * p.chunks;
   const DanWorkItem w = load_entry(p.work + blockIdx.x / groups);
@@ -248,18 +327,15 @@ void tree_attn_fwd_kernel(const KParams p) {
   const int qend = w.t0 + w.tq;
   const bool wave_work = hig < p.rep && qw0 < qend;
 
-  const TIn *qp = static_cast<const TIn *>(p.q);
-  const TIn *kp = static_cast<const TIn *>(p.k) + (int64_t)kvh * p.k_sh;
-  const TIn *vp = static_cast<const TIn *>(p.v) + (int64_t)kvh * p.v_sh;
-  const TIn *pkp = nullptr, *pvp = nullptr;
-  int64_t pk_st = 0, pv_st = 0;
+  const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
+  const TQK *pkp = nullptr;
+  int64_t pk_st = 0;
   if (P > 0) {
     const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
-    pkp = static_cast<const TIn *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
-    pvp = static_cast<const TIn *>(pd.v) + (int64_t)kvh * pd.v_stride_head;
+    pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
     pk_st = pd.k_stride_tok;
-    pv_st = pd.v_stride_tok;
   }
+  const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
 
   // Per-lane query state: lane owns query column lq of its wave. Padding
   // columns (past the tile, or an idle wave) read a clamped valid row and see
@@ -271,75 +347,74 @@ void tree_attn_fwd_kernel(const KParams p) {
   const int qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
   u32x4 qf[NK];
   {
-    const TIn *row = qp + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + 8 * hl;
+    const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + 8 * hl;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) qf[kk] = load8<TIn, TQK>(row + 16 * kk);
+    for (int kk = 0; kk < NK; ++kk) qf[kk] = load8<TQK, TQK>(row + 16 * kk);
   }
 
-  // Staging registers for the next key tile.
-  u32x4 kreg[KCH], vreg[KCH];
-  const int kc = tid % CPR;         // K: 16-byte chunk of the row
-  const int kr0 = tid / CPR;        // K: first row, then + ROWS_PER_PASS
-  const int vkg = tid % NKG;        // V: key group of KCH keys
-  const int vdc = tid / NKG;        // V: d chunk (8 values of d)
-  // Element offsets of this thread's rows from the tile's first row, for the
-  // new-token and the past tensors (a tile lying wholly in one of them is
-  // loaded from a wave-uniform base plus these loop-invariant offsets).
-  uint32_t koff_new[KCH], koff_past[KCH], voff_new[KCH], voff_past[KCH];
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
-    koff_new[i] = (uint32_t)((kr0 + i * ROWS_PER_PASS) * p.k_st + 8 * kc);
-    koff_past[i] = (uint32_t)((kr0 + i * ROWS_PER_PASS) * pk_st + 8 * kc);
-    voff_new[i] = (uint32_t)((vkg * KCH + i) * p.v_st + 8 * vdc);
-    voff_past[i] = (uint32_t)((vkg * KCH + i) * pv_st + 8 * vdc);
-  }
-
-  auto key_src = [&](const TIn *newp, int64_t new_st, const TIn *pastp, int64_t past_st, int key) -> const TIn * {
-    return key < P ? pastp + (int64_t)key * past_st : newp + (int64_t)(sg.start + key - P) * new_st;
+  // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
+  // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
+  // VF V^T blocks, and one last slot that takes a leftover K or V^T block or
+  // goes to the sink. Per-lane element offsets from the tile's first row are
+  // loop-invariant; K keeps one per source layout (new tokens / past).
+  constexpr int KF = L::kInsts / kWaves, VF = L::vInsts / kWaves;
+  constexpr int KREM = L::kInsts - KF * kWaves, VREM = L::vInsts - VF * kWaves;
+  static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
+  const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
+  const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
+  auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
+    const int pos = blk * 64 + lane;
+    return (uint32_t)(k_row(pos / KC) * st + 8 * min(pos % KC, KC - 2));
   };
-  // Key rows past the segment's end (ragged last tile) are clamped to its last
-  // row: they lie beyond every query's causal limit, so the mask zeroes their
-  // probabilities, and finite rows keep 0 * v finite.
-  auto load_tile = [&](int j) {
+  auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
+    const int pos = blk * 64 + lane;
+    return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
+  };
+  uint32_t kon[KF], kop[KF], von[VF];
+#pragma unroll
+  for (int s = 0; s < KF; ++s) {
+    kon[s] = k_offset(wave + kWaves * s, p.k_st);
+    kop[s] = k_offset(wave + kWaves * s, pk_st);
+  }
+#pragma unroll
+  for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
+  // last slot: K offsets (new, past) or the V^T / sink offset
+  const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
+  const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
+  const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
+
+  // Issue the direct loads of key tile j into stage buffer b.
+  auto issue = [&](int j, int b) __attribute__((always_inline)) {
     const int kb = j * kKeyTile;
-    const bool in_past = kb + kKeyTile <= P;
-    if (in_past || (kb >= P && kb + kKeyTile <= PN)) {  // wave-uniform fast path
-      const TIn *kt = in_past ? pkp + (int64_t)kb * pk_st : kp + (int64_t)(sg.start + kb - P) * p.k_st;
-      const TIn *vt = in_past ? pvp + (int64_t)kb * pv_st : vp + (int64_t)(sg.start + kb - P) * p.v_st;
+    uint8_t *base = smem + b * L::buf;
+    const _Float16 *vtt = vtp + kb;
+    auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
+      const int pos = blk * 64 + lane;
+      const int col = 8 * min(pos % KC, KC - 2);
+      const int key = min(kb + k_row(pos / KC), PN - 1);
+      return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
+    };
+    // (Separate loops per source layout: a select between two offset arrays
+    // would make the compiler keep them in scratch memory.)
+    if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
+      const TQK *tb = pkp + (int64_t)kb * pk_st;
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) kreg[i] = load8<TIn, TQK>(kt + (in_past ? koff_past[i] : koff_new[i]));
+      for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
+    } else if (kb >= P && kb + kKeyTile <= PN) {
+      const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) vreg[i] = load8<TIn, TPV>(vt + (in_past ? voff_past[i] : voff_new[i]));
-      return;
+      for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int key = kb + kr0 + i * ROWS_PER_PASS;
-      kreg[i] = load8<TIn, TQK>(key_src(kp, p.k_st, pkp, pk_st, min(key, PN - 1)) + 8 * kc);
-    }
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int key = kb + vkg * KCH + i;
-      vreg[i] = load8<TIn, TPV>(key_src(vp, p.v_st, pvp, pv_st, min(key, PN - 1)) + 8 * vdc);
-    }
-  };
-  auto store_tile = [&](int it) {
-    uint8_t *kb = smem + (it & 1) * KBYTES;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int m = k_row(kr0 + i * ROWS_PER_PASS);
-      *reinterpret_cast<u32x4 *>(kb + m * KROW + kc * 16) = kreg[i];
-    }
-    uint8_t *vb = smem + VBASE + (it % 3) * VBYTES;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = vdc * 8 + e;
-      if constexpr (KCH == 2) {
-        *reinterpret_cast<uint32_t *>(vb + d * VROW + vkg * 4) = half_of(vreg[0], e) | (half_of(vreg[1], e) << 16);
-      } else {
-        *reinterpret_cast<uint16_t *>(vb + d * VROW + vkg * 2) = (uint16_t)half_of(vreg[0], e);
-      }
-    }
+    for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
+    if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
+    if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
   };
 
   f32x16 o[ND];
@@ -347,67 +422,78 @@ void tree_attn_fwd_kernel(const KParams p) {
   for (int db = 0; db < ND; ++db) o[db] = f32x16{};
   float mrun = -1e30f, lsum = 0.f;
   u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
-#pragma unroll
-  for (int kj = 0; kj < 4; ++kj) pf[kj] = u32x4{0, 0, 0, 0};
 
-  // S^T = K Q^T for 64 keys x 32 queries: two 32-key blocks.
-  auto qk_phase = [&](int it, f32x16 (&s)[2]) {
-    const uint8_t *kb = smem + (it & 1) * KBYTES;
+  // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
+  auto qk_phase = [&](int b, f32x16(&s)[2]) {
+    const uint8_t *kbuf = smem + b * L::buf;
     s[0] = f32x16{};
     s[1] = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        const int m = 32 * mb + lq;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(kb + m * KROW + (2 * kk + hl) * 16);
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
         s[mb] = mfma32<TQK>(a, qf[kk], s[mb]);
       }
     }
   };
-  // Mask (boundary tiles only), online-softmax update, P^T in fp16.
-  auto softmax_phase = [&](int j, f32x16 (&s)[2]) {
-    if (j >= w.jfull) {
-      // Key index of register r relative to the tile start: 32*mb + 16*(r/8) +
-      // 8*hl + r%8. Causal limit and sibling-branch gap become per-lane bounds
-      // on that index; the gap test runs only on tiles meeting [PT, lo_max).
-      const int kb = j * kKeyTile;
-      const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
-      if (kb + kKeyTile > PT && kb < w.lo_max) {
-        const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
+  // Tree mask on boundary tiles. Key index of register r relative to the tile
+  // start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
+  // sibling-branch gap are per-lane bounds on it; the gap test runs only on
+  // tiles meeting [PT, lo_max).
+  auto mask_phase = [&](int j, f32x16(&s)[2]) {
+    if (j < w.jfull) return;
+    const int kb = j * kKeyTile;
+    const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
+    if (kb + kKeyTile > PT && kb < w.lo_max) {
+      const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-            const bool vis = rel <= lim && (rel < g0 || rel >= g1);
-            s[mb][r] = vis ? s[mb][r] : -INFINITY;
-          }
-      } else {
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+          const bool vis = rel <= lim && (rel < g0 || rel >= g1);
+          s[mb][r] = vis ? s[mb][r] : -INFINITY;
+        }
+    } else {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-            s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
-          }
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+          s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
+        }
     }
-    float mx = -INFINITY;
+  };
+  // Running max: raise it (rescaling O and l) only when the tile's max exceeds
+  // it by more than kLazyRescale, so the probabilities stay <= 2^kLazyRescale.
+  // The test needs no cross-lane exchange: a lane holds half of its query's
+  // keys and the other half sits in lane ^ 32 of the same wave, so the
+  // wave-wide vote covers both. Only a rescale combines the two halves, which
+  // keeps the running max identical in both.
+  auto max_phase = [&](f32x16(&s)[2]) {
+    float m8[8];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mc = mx * p.c;
+    for (int w2 = 4; w2 >= 1; w2 >>= 1)
+#pragma unroll
+      for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
+    const float mc = m8[0] * p.c;
     if (__any(mc > mrun + kLazyRescale)) {
-      const float mnew = fmaxf(mrun, mc);
+      const float mnew = fmaxf(mrun, fmaxf(mc, __shfl_xor(mc, 32)));
       const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
       mrun = mnew;
       lsum *= alpha;
 #pragma unroll
       for (int db = 0; db < ND; ++db) o[db] *= alpha;
     }
+  };
+  // P = exp2(S * c - m) in fp16; the normalizer sums the fp16-rounded values
+  // that P V uses (exact products, fp32 accumulation), so rounding P mostly
+  // cancels in O / l. (Pairs are taken by shuffling the whole vector: clang 22
+  // miscompiles __builtin_bit_cast applied to one element of an ext_vector.)
+  auto exp_phase = [&](f32x16(&s)[2]) {
     const float mneg = -mrun;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
@@ -417,66 +503,81 @@ void tree_attn_fwd_kernel(const KParams p) {
         x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], p.c, mneg));
         x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], p.c, mneg));
       }
-      pf[2 * mb] = pack8<TPV>(x0);
-      pf[2 * mb + 1] = pack8<TPV>(x1);
+      pf[2 * mb] = pack8<_Float16>(x0);
+      pf[2 * mb + 1] = pack8<_Float16>(x1);
     }
-    // The normalizer sums the fp16-rounded probabilities that P V uses (exact
-    // fp16 products, fp32 accumulation), so rounding P mostly cancels in O / l.
-    // (Pairs are taken with a shuffle of the whole vector: clang 22 miscompiles
-    // __builtin_bit_cast applied to a single element of an ext_vector.)
-    float acc = 0.f;
+    float acc[4];
 #pragma unroll
-    for (int kj = 0; kj < 4; ++kj) {
+    for (int kj = 0; kj < 4; ++kj) {  // four short chains instead of one long one
       const f16x8 h = __builtin_bit_cast(f16x8, pf[kj]);
-      acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), kOnes2, acc, false);
-      acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), kOnes2, acc, false);
-      acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc, false);
-      acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc, false);
+      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), kOnes2, 0.f, false);
+      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), kOnes2, acc[kj], false);
+      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc[kj], false);
+      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc[kj], false);
     }
-    lsum += acc;
+    lsum += (acc[0] + acc[1]) + (acc[2] + acc[3]);
   };
-  // O^T += V^T P^T over the tile's 64 keys.
-  auto pv_phase = [&](int it) {
-    const uint8_t *vb = smem + VBASE + (it % 3) * VBYTES;
+  // O^T += V^T P^T over the 64 keys of stage buffer b.
+  auto pv_phase = [&](int b) __attribute__((always_inline)) {
+    const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
 #pragma unroll
     for (int kj = 0; kj < 4; ++kj) {
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const int d = 32 * db + lq;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vb + d * VROW + (2 * kj + hl) * 16);
-        o[db] = mfma32<TPV>(a, pf[kj], o[db]);
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
+        o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
       }
     }
   };
 
   const int ntile = w.ja1 + (w.jb1 - w.jb0);
-  auto tile_of = [&](int i) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
+  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
+  // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (t < ntile) issue(tile_of(t), t);
+  if (ntile >= 3) wait_vmem<2 * SLOTS>();
+  else if (ntile == 2) wait_vmem<SLOTS>();
+  else wait_vmem<0>();
+  barrier_lds();
+  f32x16 sa[2], sb[2];
   if (ntile > 0) {
-    load_tile(tile_of(0));
-    store_tile(0);
+    qk_phase(0, sa);
+    mask_phase(tile_of(0), sa);
+    max_phase(sa);
   }
-  __syncthreads();
 
-  // Idle waves compute on clamped rows too: no divergent control flow around
-  // the barriers.
-  for (int it = 0; it < ntile; ++it) {
-    const int j = tile_of(it);
-    if (it + 1 < ntile) load_tile(tile_of(it + 1));
-    f32x16 s[2];
-    if (lagging) {
-      if (it > 0) pv_phase(it - 1);
-      qk_phase(it, s);
-      softmax_phase(j, s);
-    } else {
-      qk_phase(it, s);
-      softmax_phase(j, s);
-      pv_phase(it);
+  // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
+  // core, then O += V P of tile it while the VALU masks and reduces S(it+1).
+  // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
+  // barrier of step it), its buffer's previous tile it-1 is finished by every
+  // wave.
+  int it = 0;
+  auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
+    const bool has_next = it + 1 < ntile;
+    if (has_next) {
+      if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+      else wait_vmem<0>();
+      barrier_lds();
+      if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
     }
-    if (it + 1 < ntile) store_tile(it + 1);
-    __syncthreads();
+    // S of the next tile is computed unconditionally (on the last tile it
+    // reads a stale but complete buffer and is discarded) so that it shares a
+    // basic block with the softmax VALU work and the two interleave.
+    exp_phase(cur);
+    qk_phase((it + 1) & 3, nxt);
+    pv_phase(it & 3);
+    if (has_next) {
+      mask_phase(tile_of(it + 1), nxt);
+      max_phase(nxt);
+    }
+    ++it;
+  };
+  while (it < ntile) {
+    step(sa, sb);
+    if (it < ntile) step(sb, sa);
   }
-  if (lagging && ntile > 0) pv_phase(ntile - 1);
 
   // Epilogue: O = O^T / l, written token-major [N, H, D].
   const float l = lsum + __shfl_xor(lsum, 32);
@@ -504,17 +605,23 @@ int fail(int status, const char *fmt, ...) {
   return status;
 }
 
-// Heads of one kv group that one work group covers: 4 waves split over them.
-int heads_per_group(int rep) { return rep >= 3 ? 4 : rep; }  // of kWaves / 2 per group
+// Heads of one kv group that one work group covers: the 4 waves of a SIMD
+// pair's group split over them.
+int heads_per_group(int rep) { return rep >= 3 ? 4 : rep; }
 
-template <typename TIn, typename TOut, typename TQK, int D>
-hipError_t launch(const KParams &kp, int grid, hipStream_t stream) {
-  constexpr bool kSkew = DAN_TREE_ATTN_SKEW;
-  auto kernel = tree_attn_fwd_kernel<TIn, TOut, TQK, D, kSkew>;
+template <typename TV, int D>
+hipError_t launch_pack(const PackParams &pp, int blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((vt_pack_kernel<TV, D>), dim3(blocks), dim3(256), 0, stream, pp);
+  return hipGetLastError();
+}
+
+template <typename TQK, typename TOut, int D>
+hipError_t launch_attn(const KParams &kp, int grid, hipStream_t stream) {
+  auto kernel = tree_attn_kernel<TQK, TOut, D>;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, LdsLayout<D>::total);
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::total);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), LdsLayout<D>::total, stream, kp);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), Lds<D>::total, stream, kp);
   return hipGetLastError();
 }
 
@@ -531,6 +638,11 @@ int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads) {
   return dan::kWaveQ * dan::kWaves / dan::heads_per_group(num_heads / num_kv_heads);
 }
 
+int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols) {
+  if (num_kv_heads <= 0 || head_dim <= 0 || vt_cols < 0 || vt_cols % dan::kKeyTile) return 0;
+  return (int64_t)num_kv_heads * head_dim * vt_cols * 2;
+}
+
 int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   using namespace dan;
   g_err[0] = 0;
@@ -544,47 +656,59 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   const int rep = H / Hkv;
   const int tq = dan_tree_attn_tile_q(H, Hkv);
   if (a->tile_q != tq) return fail(DAN_ERR_INVALID_ARGUMENT, "tile_q %d, the kernel needs %d", a->tile_q, tq);
-  if (a->num_work < 0 || a->num_segments < 0 || a->num_pasts < 0 || a->num_tokens < 0)
+  const int in = a->in_dtype, vd = a->v_dtype, out = a->out_dtype;
+  const bool bf16 = in == DAN_DTYPE_BF16 && vd == DAN_DTYPE_BF16 && out == DAN_DTYPE_BF16;
+  const bool f16 = in == DAN_DTYPE_F16 && vd == DAN_DTYPE_F16 && out == DAN_DTYPE_F16;
+  const bool f32 = in == DAN_DTYPE_F16 && vd == DAN_DTYPE_F32 && out == DAN_DTYPE_F32;
+  if (!bf16 && !f16 && !f32)
+    return fail(DAN_ERR_UNSUPPORTED, "dtype combination q/k=%d v=%d out=%d is not built", in, vd, out);
+  if (a->num_work < 0 || a->num_segments < 0 || a->num_pasts < 0 || a->num_tokens < 0 || a->vt_cols < 0)
     return fail(DAN_ERR_INVALID_ARGUMENT, "negative count");
   if (a->num_work == 0) return DAN_OK;
-  if (!a->q || !a->k || !a->v || !a->out || !a->segments || !a->work || !a->key_lo)
+  if (!a->q || !a->k || !a->v || !a->out || !a->segments || !a->work || !a->key_lo || !a->col_seg)
     return fail(DAN_ERR_INVALID_ARGUMENT, "NULL tensor or table pointer");
   if (a->num_pasts > 0 && !a->pasts) return fail(DAN_ERR_INVALID_ARGUMENT, "num_pasts > 0 with NULL pasts");
   if (!(a->scale > 0.f) || !isfinite(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
-  // Per-thread row offsets inside a 64-key tile are kept in 32 bits.
-  const int64_t max_tok_stride = a->k_stride_tok > a->v_stride_tok ? a->k_stride_tok : a->v_stride_tok;
-  if (max_tok_stride < 0 || max_tok_stride * kKeyTile >= (int64_t(1) << 31))
-    return fail(DAN_ERR_UNSUPPORTED, "k/v token stride %lld is too large", (long long)max_tok_stride);
+  const int64_t need = dan_tree_attn_workspace_size(Hkv, D, a->vt_cols);
+  if (a->vt_cols <= 0 || need <= 0) return fail(DAN_ERR_INVALID_ARGUMENT, "vt_cols %d must be a positive multiple of %d", a->vt_cols, kKeyTile);
+  if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  // Per-lane offsets inside a tile are kept in 32 bits.
+  if (a->k_stride_tok < 0 || a->k_stride_tok * kKeyTile >= (int64_t(1) << 31) || (int64_t)D * a->vt_cols >= (int64_t(1) << 31))
+    return fail(DAN_ERR_UNSUPPORTED, "k token stride %lld or vt_cols %d is too large", (long long)a->k_stride_tok, a->vt_cols);
   const int hpw = heads_per_group(rep);
   const int chunks = (rep + hpw - 1) / hpw;
   const int64_t grid = (int64_t)a->num_work * Hkv * chunks;
-  if (grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "grid of %lld work groups is too large", (long long)grid);
+  const int64_t pack_grid = (int64_t)(a->vt_cols / kKeyTile) * Hkv;
+  if (grid > 0x7fffffff || pack_grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "grid is too large");
+
+  PackParams pp;
+  pp.v = a->v; pp.v_st = a->v_stride_tok; pp.v_sh = a->v_stride_head;
+  pp.segs = a->segments; pp.pasts = a->pasts; pp.col_seg = a->col_seg;
+  pp.vt = static_cast<_Float16 *>(a->workspace);
+  pp.num_kv_heads = Hkv; pp.vt_cols = a->vt_cols;
 
   KParams kp;
-  kp.q = a->q; kp.k = a->k; kp.v = a->v; kp.o = a->out;
+  kp.q = a->q; kp.k = a->k; kp.o = a->out; kp.vt = pp.vt;
   kp.q_st = a->q_stride_tok; kp.q_sh = a->q_stride_head;
   kp.k_st = a->k_stride_tok; kp.k_sh = a->k_stride_head;
-  kp.v_st = a->v_stride_tok; kp.v_sh = a->v_stride_head;
   kp.o_st = a->o_stride_tok; kp.o_sh = a->o_stride_head;
   kp.segs = a->segments; kp.pasts = a->pasts; kp.work = a->work; kp.key_lo = a->key_lo;
-  kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks;
+  kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
   kp.c = a->scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool d128 = D == 128;
   hipError_t err;
-  const int in = a->in_dtype, out = a->out_dtype;
-  if (in == DAN_DTYPE_BF16 && out == DAN_DTYPE_BF16) {
-    err = D == 128 ? launch<__bf16, __bf16, __bf16, 128>(kp, (int)grid, s) : launch<__bf16, __bf16, __bf16, 64>(kp, (int)grid, s);
-  } else if (in == DAN_DTYPE_F16 && out == DAN_DTYPE_F16) {
-    err = D == 128 ? launch<_Float16, _Float16, _Float16, 128>(kp, (int)grid, s)
-                   : launch<_Float16, _Float16, _Float16, 64>(kp, (int)grid, s);
-  } else if (in == DAN_DTYPE_F32 && out == DAN_DTYPE_F32) {
-    err = D == 128 ? launch<float, float, _Float16, 128>(kp, (int)grid, s)
-                   : launch<float, float, _Float16, 64>(kp, (int)grid, s);
-  } else {
-    return fail(DAN_ERR_UNSUPPORTED, "dtype combination in=%d out=%d is not built", in, out);
-  }
-  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  if (bf16) err = d128 ? launch_pack<__bf16, 128>(pp, (int)pack_grid, s) : launch_pack<__bf16, 64>(pp, (int)pack_grid, s);
+  else if (f16) err = d128 ? launch_pack<_Float16, 128>(pp, (int)pack_grid, s) : launch_pack<_Float16, 64>(pp, (int)pack_grid, s);
+  else err = d128 ? launch_pack<float, 128>(pp, (int)pack_grid, s) : launch_pack<float, 64>(pp, (int)pack_grid, s);
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "V^T pack launch failed: %s", hipGetErrorString(err));
+
+  if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, (int)grid, s) : launch_attn<__bf16, __bf16, 64>(kp, (int)grid, s);
+  else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, (int)grid, s) : launch_attn<_Float16, _Float16, 64>(kp, (int)grid, s);
+  else err = d128 ? launch_attn<_Float16, float, 128>(kp, (int)grid, s) : launch_attn<_Float16, float, 64>(kp, (int)grid, s);
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
 }
 

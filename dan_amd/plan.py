@@ -11,6 +11,10 @@ calls. Here the same segment metadata becomes:
   ``kc <= qc and (kc < P + trunk or kc >= key_lo[query])``, which is the tree
   mask of dan/attention.py:54-59 with the past prepended as all-visible
   columns (dan/attention.py:86-95, :259-264);
+- the V^T column plan: each segment owns a 64-aligned range of
+  ``roundup(P + n, 64)`` columns (``vt_col``) of the fp16 V^T copy the kernel's
+  pre-pass writes, holding its [past; new] keys in segment key coordinates;
+  ``col_seg`` maps every 64-column block to its segment;
 - a work list of query tiles (``tile_q`` queries of one segment). Each item
   lists the key tiles (64 keys) any of its queries can see -- the trunk (and
   past) range, then the branch range starting at the earliest branch start in
@@ -59,7 +63,8 @@ def validate_segments(segments, num_tokens):
 
 def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
     """Host tables for the kernel. Returns (segs [S,8] int32, work [W,8] int32,
-    key_lo [N] int32, cost [W] int64, past_dicts).
+    key_lo [N] int32, cost [W] int64, past_dicts, col_seg [C] int32) with
+    C * key_tile the V^T column count.
 
     ``past_dicts`` lists the distinct prefix-cache entries (by identity) in
     the order the segment table's past index refers to them."""
@@ -69,7 +74,7 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
     segs = np.zeros((len(segments), 8), np.int32)
     key_lo = np.zeros(num_tokens, np.int32)
     past_dicts, past_index = [], {}
-    items = []
+    items, col_seg = [], []
     for i, s in enumerate(segments):
         n, t = s.end - s.start, s.trunk
         p = s.past_len if s.past else 0
@@ -78,7 +83,8 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
             pidx = past_index.setdefault(id(s.past), len(past_dicts))
             if pidx == len(past_dicts):
                 past_dicts.append(s.past)
-        segs[i, :5] = (s.start, n, t, p, pidx)
+        segs[i, :6] = (s.start, n, t, p, pidx, len(col_seg) * key_tile)
+        col_seg += [i] * _ceil_div(p + n, key_tile)
         for a, b in s.branches:
             key_lo[a:b] = p + (a - s.start)
         pt = p + t
@@ -99,7 +105,7 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
     work = np.array(items, np.int32).reshape(-1, 8)
     cost = (work[:, 3].astype(np.int64) + work[:, 5] - work[:, 4]) if len(work) else np.zeros(0, np.int64)
     order = np.argsort(-cost, kind="stable")
-    return segs, work[order], key_lo, cost[order], past_dicts
+    return segs, work[order], key_lo, cost[order], past_dicts, np.array(col_seg, np.int32)
 
 
 @dataclass
@@ -114,21 +120,29 @@ class TilePlan:
     key_lo: np.ndarray
     cost: np.ndarray
     past_dicts: list
+    col_seg: np.ndarray = None
     segs_d: object = None
     work_d: object = None
     key_lo_d: object = None
+    col_seg_d: object = None
     past_tables: dict = field(default_factory=dict)  # layer -> (device bytes, keep-alive refs)
+    workspace: dict = field(default_factory=dict)  # bytes -> device scratch (reused by every layer)
 
     @classmethod
     def build(cls, segments, num_tokens, tile_q, device):
         import torch
 
-        segs, work, key_lo, cost, past_dicts = build_tables(segments, num_tokens, tile_q)
-        plan = cls(tile_q, num_tokens, torch.device(device), segs, work, key_lo, cost, past_dicts)
+        segs, work, key_lo, cost, past_dicts, col_seg = build_tables(segments, num_tokens, tile_q)
+        plan = cls(tile_q, num_tokens, torch.device(device), segs, work, key_lo, cost, past_dicts, col_seg)
         plan.segs_d = _upload(segs, device)
         plan.work_d = _upload(work, device)
         plan.key_lo_d = _upload(key_lo, device)
+        plan.col_seg_d = _upload(col_seg, device)
         return plan
+
+    @property
+    def vt_cols(self):
+        return int(len(self.col_seg) * KEY_TILE)
 
     def matches(self, num_tokens, tile_q, device):
         import torch

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 1
+#define DAN_TREE_ATTN_ABI_VERSION 2
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -53,7 +53,7 @@ typedef enum {
 typedef enum {
   DAN_DTYPE_BF16 = 0,
   DAN_DTYPE_F16 = 1,
-  DAN_DTYPE_F32 = 2,  /* fp32 in/out; staged to fp16 for the matrix cores */
+  DAN_DTYPE_F32 = 2,  /* v and out only (q and k of an fp32 model are passed as fp16) */
   DAN_DTYPE_E4M3 = 3  /* OCP float8 e4m3fn inputs with per-tensor fp32 scales */
 } DanDtype;
 
@@ -66,7 +66,10 @@ typedef struct {
   int32_t trunk;
   int32_t past_len; /* P: cached prefix tokens before the trunk (0: none) */
   int32_t past_idx; /* index into DanTreeAttnArgs.pasts, -1 when past_len == 0 */
-  int32_t reserved[3];
+  int32_t vt_col;   /* first column of this segment in the workspace's V^T copy
+                       (a multiple of DAN_TREE_ATTN_KEY_TILE); the segment owns
+                       roundup(past_len + n) columns from there */
+  int32_t reserved[2];
 } DanSegmentDesc;
 
 /* One prefix-cache entry for the current layer: k, v each [Hkv, len, D]
@@ -107,8 +110,9 @@ typedef struct {
 
 typedef struct {
   int32_t abi_version; /* DAN_TREE_ATTN_ABI_VERSION */
-  int32_t in_dtype;    /* DanDtype of q, k, v and the pasts */
+  int32_t in_dtype;    /* DanDtype of q, k and the pasts' k: bf16 or f16 */
   int32_t out_dtype;   /* DanDtype of out: bf16, f16 or f32 */
+  int32_t v_dtype;     /* DanDtype of v and the pasts' v: bf16, f16 or f32 */
   int32_t num_heads;   /* H */
   int32_t num_kv_heads;/* Hkv; query head h reads kv head h / (H / Hkv) */
   int32_t head_dim;    /* D: 64 or 128 */
@@ -133,13 +137,24 @@ typedef struct {
    *   kc <= qc  and  (kc < P + trunk  or  kc >= key_lo[query]). */
   const int32_t *key_lo;
   int32_t tile_q; /* queries per work item; must equal dan_tree_attn_tile_q() */
-  int32_t reserved;
+  int32_t vt_cols; /* columns of the V^T copy: sum over segments of roundup(past_len + n) */
+  /* [vt_cols / DAN_TREE_ATTN_KEY_TILE]: the segment owning each column block */
+  const int32_t *col_seg;
+  /* Device scratch of at least dan_tree_attn_workspace_size() bytes, 256-byte
+   * aligned, owned by the caller: it receives V (and the pasts' v) as fp16,
+   * transposed to [Hkv][D][vt_cols], before the attention kernel runs on the
+   * same stream. */
+  void *workspace;
+  int64_t workspace_bytes;
 } DanTreeAttnArgs;
 
 /* Fused tree-masked attention forward: out = softmax(scale * q k^T + mask) v
  * over every (query, visible key) pair of every segment, in one launch.
  * Replaces dan/attention.py:200-241 (attend -> _attend_varlen) on gfx950. */
 int dan_tree_attn_fwd(const DanTreeAttnArgs *args, void *stream);
+
+/* Bytes of workspace dan_tree_attn_fwd needs (0 for invalid arguments). */
+int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols);
 
 /* Queries per work item the kernel expects for this head configuration
  * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172).

@@ -85,7 +85,7 @@ def test_abi_version_and_tile_q(lib):
 def _args(**kw):
     a = _native.DanTreeAttnArgs()
     a.abi_version = _native.ABI_VERSION
-    a.in_dtype = a.out_dtype = _native.DTYPE_BF16
+    a.in_dtype = a.out_dtype = a.v_dtype = _native.DTYPE_BF16
     a.num_heads, a.num_kv_heads, a.head_dim, a.num_tokens = 32, 8, 128, 16
     a.scale = 0.088
     a.tile_q = 64
@@ -119,11 +119,23 @@ def test_empty_work_is_a_no_op(lib):
     assert _native.last_error(lib) == ""
 
 
-def test_bad_scale_and_dtype(lib):
-    x = ctypes.c_int(0)
-    p = ctypes.addressof(x)
-    full = dict(num_work=1, q=p, k=p, v=p, out=p, segments=p, work=p, key_lo=p)
+def test_workspace_size(lib):
+    assert _native.workspace_size(8, 128, 640, lib) == 8 * 128 * 640 * 2
+    assert _native.workspace_size(8, 128, 100, lib) == 0  # not a multiple of the key tile
+    assert _native.workspace_size(0, 128, 64, lib) == 0
+
+
+def test_bad_scale_dtype_and_workspace(lib):
+    x = (ctypes.c_uint8 * 4096)()
+    p = (ctypes.addressof(x) + 255) // 256 * 256
+    full = dict(num_work=1, q=p, k=p, v=p, out=p, segments=p, work=p, key_lo=p, col_seg=p, vt_cols=64,
+                workspace=p, workspace_bytes=8 * 128 * 64 * 2)
     assert lib.dan_tree_attn_fwd(ctypes.byref(_args(scale=0.0, **full)), None) == _native.ERR_INVALID_ARGUMENT
     assert "scale" in _native.last_error(lib)
-    bad = _args(in_dtype=_native.DTYPE_BF16, out_dtype=_native.DTYPE_F32, **full)
+    small = dict(full, workspace_bytes=100)
+    assert lib.dan_tree_attn_fwd(ctypes.byref(_args(**small)), None) == _native.ERR_INVALID_ARGUMENT
+    assert "workspace" in _native.last_error(lib)
+    odd = dict(full, vt_cols=100)
+    assert lib.dan_tree_attn_fwd(ctypes.byref(_args(**odd)), None) == _native.ERR_INVALID_ARGUMENT
+    bad = _args(**dict(full, v_dtype=_native.DTYPE_E4M3))
     assert lib.dan_tree_attn_fwd(ctypes.byref(bad), None) == _native.ERR_UNSUPPORTED

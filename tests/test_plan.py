@@ -15,7 +15,16 @@ from oracle import tree_attention as O
 
 
 def check_plan(segments, num_tokens, tile_q):
-    segs, work, key_lo, cost, past_dicts = build_tables(segments, num_tokens, tile_q)
+    segs, work, key_lo, cost, past_dicts, col_seg = build_tables(segments, num_tokens, tile_q)
+    # V^T columns: each segment owns a 64-aligned range of roundup(P + n) columns, in order
+    col = 0
+    for i, s in enumerate(segments):
+        p = s.past_len if s.past else 0
+        assert segs[i, 5] == col and col % KEY_TILE == 0
+        span = _ceil(p + s.end - s.start, KEY_TILE)
+        assert (col_seg[col // KEY_TILE: col // KEY_TILE + span] == i).all()
+        col += span * KEY_TILE
+    assert len(col_seg) * KEY_TILE == col
     assert (np.diff(cost) <= 0).all(), "work list must be sorted longest first"
     covered = np.zeros(num_tokens, int)
     for item in work:
@@ -97,7 +106,7 @@ def test_plan_random_trees(seed, tile_q):
 
 def test_shared_past_entries_are_deduplicated():
     w = W.config3(0)
-    segs, _, _, _, past_dicts = build_tables(w.segments, w.num_tokens, 64)
+    segs, _, _, _, past_dicts, _ = build_tables(w.segments, w.num_tokens, 64)
     assert len(past_dicts) == 1 and past_dicts[0] is w.segments[0].past
 
 
