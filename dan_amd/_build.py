@@ -9,6 +9,9 @@ Flags:
   -target-feature -packed-fp32-ops no packed fp32 VALU instructions.
   -amdgpu-mfma-vgpr-form           matrix-core results in VGPRs, so the softmax
                                    reads the score tile without AGPR copies.
+  -fno-honor-nans -mno-amdgpu-ieee v_max_f32 without a canonicalizing max in
+                                   front of every operand (the row max is the
+                                   softmax's largest VALU cost after exp).
 """
 import os
 import shutil
@@ -27,6 +30,7 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-fno-honor-nans", "-mno-amdgpu-ieee",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 

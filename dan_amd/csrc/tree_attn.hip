@@ -49,6 +49,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "dan_tree_attn.h"
 
 namespace dan {
@@ -80,7 +82,7 @@ struct KParams {
   const DanPastDesc *pasts;
   const DanWorkItem *work;
   const int32_t *key_lo;
-  int32_t num_kv_heads, rep, hpw, chunks, vt_cols;
+  int32_t num_kv_heads, rep, hpw, chunks, vt_cols, num_tokens;
   float c;  // softmax scale * log2(e)
 };
 
@@ -108,8 +110,8 @@ __device__ inline DAN_GLOBAL T *gbl_mut(T *p) {
   return (DAN_GLOBAL T *)p;
 }
 
-// A small table entry read from global memory (dword by dword; the compiler
-// merges the loads).
+// A small table entry at a wave-uniform address, read from global memory
+// dword by dword (the compiler merges the loads) and moved to scalar registers.
 template <typename T>
 __device__ inline T load_entry(const T *p) {
   static_assert(sizeof(T) % 4 == 0, "table entries are dword multiples");
@@ -118,7 +120,7 @@ __device__ inline T load_entry(const T *p) {
   } raw;
   const DAN_GLOBAL uint32_t *src = gbl(reinterpret_cast<const uint32_t *>(p));
 #pragma unroll
-  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = src[i];
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
   return __builtin_bit_cast(T, raw);
 }
 
@@ -204,6 +206,15 @@ __device__ inline uint32_t half_of(u32x4 v, int e) {
 // of its 32-key block -- exactly the k-order of the P^T B operand.
 __device__ inline int k_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
+
+// A wave-uniform 64-bit value (pointer or integer), moved to scalar registers.
+template <typename T>
+__device__ inline T uniform64(T x) {
+  static_assert(sizeof(T) == 8, "64-bit values");
+  const uint64_t v = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+}
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone).
 template <int N>
@@ -327,14 +338,21 @@ void tree_attn_kernel(const KParams p) {
   const int qend = w.t0 + w.tq;
   const bool wave_work = hig < p.rep && qw0 < qend;
 
-  const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
-  const TQK *pkp = nullptr;
-  int64_t pk_st = 0;
+  // K sources in bytes: key coordinate x < P is row x of the prefix-cache
+  // entry, x >= P is token row start + x - P of k. knew0 is where key
+  // coordinate 0 would sit in k's layout (only ever offset to x >= P).
+  const int64_t k_stb = p.k_st * (int64_t)sizeof(TQK);
+  const uint8_t *knew0 = uniform64(reinterpret_cast<const uint8_t *>(static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh) +
+                                   ((int64_t)sg.start - P) * k_stb);
+  const uint8_t *kpast0 = nullptr;
+  int64_t pk_stb = 0;
   if (P > 0) {
     const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
-    pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
-    pk_st = pd.k_stride_tok;
+    kpast0 = reinterpret_cast<const uint8_t *>(static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head);
+    pk_stb = pd.k_stride_tok * (int64_t)sizeof(TQK);
   }
+  kpast0 = uniform64(kpast0);
+  pk_stb = uniform64(pk_stb);
   const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
 
   // Per-lane query state: lane owns query column lq of its wave. Padding
@@ -352,6 +370,9 @@ void tree_attn_kernel(const KParams p) {
     for (int kk = 0; kk < NK; ++kk) qf[kk] = load8<TQK, TQK>(row + 16 * kk);
   }
 
+  const int ntile = w.ja1 + (w.jb1 - w.jb0);
+  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
+
   // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
   // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
   // VF V^T blocks, and one last slot that takes a leftover K or V^T block or
@@ -362,59 +383,102 @@ void tree_attn_kernel(const KParams p) {
   static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
   const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
   const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
-  auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
+  // Byte offsets (unsigned 32-bit: the loads take a wave-uniform 64-bit base in
+  // scalar registers plus this per-lane offset).
+  auto k_offset = [&](int blk, int64_t stb) __attribute__((always_inline)) {
     const int pos = blk * 64 + lane;
-    return (uint32_t)(k_row(pos / KC) * st + 8 * min(pos % KC, KC - 2));
+    return (uint32_t)(k_row(pos / KC) * stb + 8 * min(pos % KC, KC - 2) * (int)sizeof(TQK));
   };
   auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
     const int pos = blk * 64 + lane;
-    return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
+    return (uint32_t)(((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2)) * 2);
   };
-  uint32_t kon[KF], kop[KF], von[VF];
+  // Per-slot offsets: offn is the offset from the tile base (new keys' K or
+  // V^T), offx = offn ^ (past keys' K offset) for K slots and 0 otherwise,
+  // so a past tile takes offn ^ offx without a select between arrays.
+  const bool last_k = last_kind == 0;
+  uint32_t offn[SLOTS], offx[SLOTS];
 #pragma unroll
-  for (int s = 0; s < KF; ++s) {
-    kon[s] = k_offset(wave + kWaves * s, p.k_st);
-    kop[s] = k_offset(wave + kWaves * s, pk_st);
-  }
-#pragma unroll
-  for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
-  // last slot: K offsets (new, past) or the V^T / sink offset
-  const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
-  const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
-  const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
-
-  // Issue the direct loads of key tile j into stage buffer b.
-  auto issue = [&](int j, int b) __attribute__((always_inline)) {
-    const int kb = j * kKeyTile;
-    uint8_t *base = smem + b * L::buf;
-    const _Float16 *vtt = vtp + kb;
-    auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
-      const int pos = blk * 64 + lane;
-      const int col = 8 * min(pos % KC, KC - 2);
-      const int key = min(kb + k_row(pos / KC), PN - 1);
-      return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
-    };
-    // (Separate loops per source layout: a select between two offset arrays
-    // would make the compiler keep them in scratch memory.)
-    if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
-      const TQK *tb = pkp + (int64_t)kb * pk_st;
-#pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
-    } else if (kb >= P && kb + kKeyTile <= PN) {
-      const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
-#pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
+  for (int s = 0; s < SLOTS; ++s) {
+    if (s < KF) {
+      offn[s] = k_offset(wave + kWaves * s, k_stb);
+      offx[s] = offn[s] ^ k_offset(wave + kWaves * s, pk_stb);
+    } else if (s < KF + VF) {
+      offn[s] = v_offset(wave + kWaves * (s - KF));
+      offx[s] = 0;
+    } else if (last_k) {
+      offn[s] = k_offset(last_blk, k_stb);
+      offx[s] = offn[s] ^ k_offset(last_blk, pk_stb);
     } else {
-#pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
+      offn[s] = last_kind == 1 ? v_offset(last_blk - L::kInsts) : (uint32_t)((lane & 7) * 16);  // sink: any V^T address
+      offx[s] = 0;
     }
+  }
+
+  // Direct loads of tile t. On the common path (a whole tile of past keys or
+  // of new keys, inside the batch's rows) the sources are wave-uniform bases
+  // plus the per-lane offsets above, and the slots are issued one at a time
+  // between the matrix instructions of the next step (fire), so the eight
+  // waves do not queue their loads behind the barrier at once. A tile that
+  // straddles the past/new boundary or the end of the batch's rows is issued
+  // at once by prep, per lane; its fire slots, like those of the dummy tiles
+  // past the last one, then load 1 KB of V^T that stays cached into the
+  // sink. Every step thus issues at least SLOTS loads per wave after the
+  // loads of its tile, which is all the vmcnt waits below rely on.
+  struct Tile {
+    const uint8_t *kb, *vb;  // K and V^T tile bases
+    uint32_t pmask;          // ~0: past keys
+    bool dead;               // fire slots are dummies
+  };
+  const uint8_t *vt_u8 = reinterpret_cast<const uint8_t *>(vtp);
+  const uint32_t lane16 = 16 * lane;
+  auto slot_dst = [&](int s, int b, bool dead) __attribute__((always_inline)) {
+    const int blk = s < KF ? wave + kWaves * s : s < KF + VF ? L::kInsts + wave + kWaves * (s - KF) : last_blk;
+    const bool sink = dead || (s == SLOTS - 1 && last_kind == 2);
+    return sink ? smem + L::sink : smem + b * L::buf + blk * 1024;
+  };
+  auto prep = [&](int t) __attribute__((always_inline)) {
+    Tile r;
+    r.kb = r.vb = vt_u8;
+    r.pmask = 0;
+    r.dead = true;
+    if (t < ntile) {
+      const int b = t & 3;
+      const int kb = tile_of(t) * kKeyTile;
+      r.vb = vt_u8 + 2 * kb;
+      if (kb + kKeyTile <= P) {
+        r.kb = kpast0 + kb * pk_stb;
+        r.pmask = ~0u;
+        r.dead = false;
+      } else if (kb >= P && sg.start + kb - P + kKeyTile <= p.num_tokens) {
+        // Rows past the segment's end belong to the next segment; those keys
+        // are after every query of this segment, so the causal mask hides them.
+        r.kb = knew0 + kb * k_stb;
+        r.dead = false;
+      } else {
+        auto k_slow = [&](int blk) __attribute__((always_inline)) {
+          const int pos = blk * 64 + lane;
+          const int col = 8 * min(pos % KC, KC - 2) * (int)sizeof(TQK);
+          const int key = min(kb + k_row(pos / KC), PN - 1);
+          return (key < P ? kpast0 + key * pk_stb : knew0 + key * k_stb) + col;
+        };
 #pragma unroll
-    for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
-    if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
-    if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
+        for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), slot_dst(s, b, false));
+#pragma unroll
+        for (int s = KF; s < KF + VF; ++s) load_to_lds(r.vb + offn[s], slot_dst(s, b, false));
+        if (last_k) load_to_lds(k_slow(last_blk), slot_dst(SLOTS - 1, b, false));
+        else load_to_lds(r.vb + offn[SLOTS - 1], slot_dst(SLOTS - 1, b, false));
+      }
+    }
+    r.kb = uniform64(r.kb);
+    r.vb = uniform64(r.vb);
+    return r;
+  };
+  auto fire = [&](const Tile &tl, int s, int b) __attribute__((always_inline)) {
+    const bool k = s < KF || (s == SLOTS - 1 && last_k);
+    const uint32_t off = offn[s] ^ (offx[s] & tl.pmask);
+    const uint8_t *src = tl.dead ? vt_u8 + lane16 : (k ? tl.kb : tl.vb) + off;
+    load_to_lds(src, slot_dst(s, b, tl.dead));
   };
 
   f32x16 o[ND];
@@ -424,46 +488,27 @@ void tree_attn_kernel(const KParams p) {
   u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
   // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
-  auto qk_phase = [&](int b, f32x16(&s)[2]) {
-    const uint8_t *kbuf = smem + b * L::buf;
-    s[0] = f32x16{};
-    s[1] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
-        s[mb] = mfma32<TQK>(a, qf[kk], s[mb]);
-      }
-    }
+  // Tree mask on boundary tiles (j >= jfull). Key index of register r relative
+  // to the tile start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
+  // sibling-branch gap are per-lane bounds on it: visible iff rel <= lim and
+  // not g0 <= rel < g1 (the gap is empty unless the tile meets [PT, lo_max)).
+  // The mask is applied where S is read (max and exp), never written back, so
+  // S stays in the registers the matrix core wrote.
+  struct Bounds {
+    int lim, g0, g1;
   };
-  // Tree mask on boundary tiles. Key index of register r relative to the tile
-  // start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
-  // sibling-branch gap are per-lane bounds on it; the gap test runs only on
-  // tiles meeting [PT, lo_max).
-  auto mask_phase = [&](int j, f32x16(&s)[2]) {
-    if (j < w.jfull) return;
+  auto bounds = [&](int j) __attribute__((always_inline)) {
     const int kb = j * kKeyTile;
-    const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
-    if (kb + kKeyTile > PT && kb < w.lo_max) {
-      const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-          const bool vis = rel <= lim && (rel < g0 || rel >= g1);
-          s[mb][r] = vis ? s[mb][r] : -INFINITY;
-        }
-    } else {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-          s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
-        }
-    }
+    Bounds m;
+    m.lim = qk - kb - 8 * hl;
+    const bool gap = kb + kKeyTile > PT && kb < w.lo_max;
+    m.g0 = gap ? PT - kb - 8 * hl : 0;
+    m.g1 = gap ? qlo - kb - 8 * hl : 0;
+    return m;
+  };
+  auto vis = [](const Bounds &m, int mb, int r) __attribute__((always_inline)) {
+    const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+    return rel <= m.lim && (rel < m.g0 || rel >= m.g1);
   };
   // Running max: raise it (rescaling O and l) only when the tile's max exceeds
   // it by more than kLazyRescale, so the probabilities stay <= 2^kLazyRescale.
@@ -471,10 +516,15 @@ void tree_attn_kernel(const KParams p) {
   // keys and the other half sits in lane ^ 32 of the same wave, so the
   // wave-wide vote covers both. Only a rescale combines the two halves, which
   // keeps the running max identical in both.
-  auto max_phase = [&](f32x16(&s)[2]) {
+  auto max_phase = [&](const f32x16(&s)[2], bool masked, const Bounds &m) __attribute__((always_inline)) {
+    float x[32];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[16 * mb + r] = (!masked || vis(m, mb, r)) ? s[mb][r] : -INFINITY;
     float m8[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
+    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(x[4 * i], x[4 * i + 1]), fmaxf(x[4 * i + 2], x[4 * i + 3]));
 #pragma unroll
     for (int w2 = 4; w2 >= 1; w2 >>= 1)
 #pragma unroll
@@ -489,19 +539,21 @@ void tree_attn_kernel(const KParams p) {
       for (int db = 0; db < ND; ++db) o[db] *= alpha;
     }
   };
-  // P = exp2(S * c - m) in fp16; the normalizer sums the fp16-rounded values
-  // that P V uses (exact products, fp32 accumulation), so rounding P mostly
-  // cancels in O / l. (Pairs are taken by shuffling the whole vector: clang 22
-  // miscompiles __builtin_bit_cast applied to one element of an ext_vector.)
-  auto exp_phase = [&](f32x16(&s)[2]) {
+  // P = exp2(S * c - m) in fp16 (0 where masked); the normalizer sums the
+  // fp16-rounded values that P V uses (exact products, fp32 accumulation), so
+  // rounding P mostly cancels in O / l. (Pairs are taken by shuffling the whole
+  // vector: clang 22 miscompiles __builtin_bit_cast applied to one element of
+  // an ext_vector.)
+  auto exp_phase = [&](const f32x16(&s)[2], bool masked, const Bounds &m) __attribute__((always_inline)) {
     const float mneg = -mrun;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       f32x8 x0, x1;
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], p.c, mneg));
-        x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], p.c, mneg));
+        const float a0 = fmaf(s[mb][r], p.c, mneg), a1 = fmaf(s[mb][r + 8], p.c, mneg);
+        x0[r] = __builtin_amdgcn_exp2f((!masked || vis(m, mb, r)) ? a0 : -INFINITY);
+        x1[r] = __builtin_amdgcn_exp2f((!masked || vis(m, mb, r + 8)) ? a1 : -INFINITY);
       }
       pf[2 * mb] = pack8<_Float16>(x0);
       pf[2 * mb + 1] = pack8<_Float16>(x1);
@@ -517,67 +569,107 @@ void tree_attn_kernel(const KParams p) {
     }
     lsum += (acc[0] + acc[1]) + (acc[2] + acc[3]);
   };
-  // O^T += V^T P^T over the 64 keys of stage buffer b.
-  auto pv_phase = [&](int b) __attribute__((always_inline)) {
-    const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
+  f32x16 sc[2];  // S^T of one key tile: 64 keys x this wave's 32 queries
+  // S^T = K Q^T for the 64 keys of stage buffer b (prologue only).
+  auto qk_phase = [&](int b) __attribute__((always_inline)) {
+    const uint8_t *kbuf = smem + b * L::buf;
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
 #pragma unroll
-    for (int kj = 0; kj < 4; ++kj) {
+    for (int kk = 0; kk < NK; ++kk)
 #pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
-        o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
+      for (int mb = 0; mb < 2; ++mb) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
+        sc[mb] = mfma32<TQK>(a, qf[kk], sc[mb]);
       }
+  };
+  // Matrix phase of step n: S^T(n+1) = K Q^T from stage buffer qb and
+  // O^T += V^T P^T(n) from stage buffer pb, the two MFMA streams interleaved
+  // (six independent accumulator chains), with the direct loads of tile n+3
+  // issued one slot at a time in between. On the last tile S is computed from
+  // a stale but complete buffer and discarded, which keeps the block free of
+  // branches.
+  auto mma_phase = [&](int qb, int pb, const Tile &tl, int fb) __attribute__((always_inline)) {
+    const uint8_t *kbuf = smem + qb * L::buf;
+    const uint8_t *vbuf = smem + pb * L::buf + L::kBytes;
+    constexpr int NQ = 2 * NK, NP = 4 * ND;
+    static_assert(NQ == NP, "QK and PV issue the same number of MFMAs");
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (i % 3 == 0 && i / 3 < SLOTS) fire(tl, i / 3, fb);
+      const int kk = i >> 1, mb = i & 1;
+      const u32x4 ka = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
+      sc[mb] = mfma32<TQK>(ka, qf[kk], sc[mb]);
+      const int kj = i / ND, db = i % ND;
+      const u32x4 va = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
+      o[db] = mfma32<_Float16>(va, pf[kj], o[db]);
+    }
+#pragma unroll
+    for (int sl = (NQ + 2) / 3; sl < SLOTS; ++sl) fire(tl, sl, fb);
+    // Schedule: operand reads run two MFMA pairs ahead of their use (enough
+    // to cover LDS latency at one MFMA per 32 cycles, without holding more
+    // than four fragments in registers); each direct load follows the MFMA
+    // pair it was written beside.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads of pairs 0, 1
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (i % 3 == 0 && i / 3 < SLOTS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                             // MFMA
+      if (i + 2 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                            // DS reads
     }
   };
-
-  const int ntile = w.ja1 + (w.jb1 - w.jb0);
-  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
+  // Softmax of tile t (VALU only): running max, then P in fp16.
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const int j = tile_of(t);
+    if (j >= w.jfull) {
+      const Bounds m = bounds(j);
+      max_phase(sc, true, m);
+      exp_phase(sc, true, m);
+    } else {
+      max_phase(sc, false, Bounds{});
+      exp_phase(sc, false, Bounds{});
+    }
+  };
 
   // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
 #pragma unroll
-  for (int t = 0; t < 3; ++t)
-    if (t < ntile) issue(tile_of(t), t);
-  if (ntile >= 3) wait_vmem<2 * SLOTS>();
-  else if (ntile == 2) wait_vmem<SLOTS>();
-  else wait_vmem<0>();
+  for (int t = 0; t < 3; ++t) {
+    const Tile tl = prep(t);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) fire(tl, s, t);
+  }
+  wait_vmem<2 * SLOTS>();
   barrier_lds();
-  f32x16 sa[2], sb[2];
-  if (ntile > 0) {
-    qk_phase(0, sa);
-    mask_phase(tile_of(0), sa);
-    max_phase(sa);
-  }
+  if (ntile > 0) qk_phase(0);
 
-  // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
-  // core, then O += V P of tile it while the VALU masks and reduces S(it+1).
-  // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
-  // barrier of step it), its buffer's previous tile it-1 is finished by every
-  // wave.
-  int it = 0;
-  auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
-    const bool has_next = it + 1 < ntile;
-    if (has_next) {
-      if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
-      else wait_vmem<0>();
+  // Step n (one barrier each): softmax of tile n (VALU), then the matrix
+  // phase M(n) = {S(n+1) = K Q^T, O += V P(n)}. Trailing waves pass the
+  // step's barrier before their softmax, leading waves after it, so on every
+  // SIMD one wave works on the VALU while the other keeps the matrix core
+  // busy.
+  // Stage buffer of tile t is t % 4: the loads of tile n+3 (issued during
+  // M(n), after the barrier) go to the buffer of tile n-1, whose last reader,
+  // M(n-1), precedes the barrier in both wave groups. The wait before the
+  // barrier leaves outstanding only loads issued after tile n+1's.
+  const bool lead = wave < kWaves / 2;  // one leading and one trailing wave per SIMD
+  for (int n = 0; n < ntile; ++n) {
+    if (!lead) {
+      wait_vmem<SLOTS>();
       barrier_lds();
-      if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
     }
-    // S of the next tile is computed unconditionally (on the last tile it
-    // reads a stale but complete buffer and is discarded) so that it shares a
-    // basic block with the softmax VALU work and the two interleave.
-    exp_phase(cur);
-    qk_phase((it + 1) & 3, nxt);
-    pv_phase(it & 3);
-    if (has_next) {
-      mask_phase(tile_of(it + 1), nxt);
-      max_phase(nxt);
+    softmax(n);
+    if (lead) {
+      wait_vmem<SLOTS>();
+      barrier_lds();
     }
-    ++it;
-  };
-  while (it < ntile) {
-    step(sa, sb);
-    if (it < ntile) step(sb, sa);
+    const Tile tl = prep(n + 3);
+    mma_phase((n + 1) & 3, n & 3, tl, (n + 3) & 3);
   }
+  // The trailing steps' loads (into the sink) must land before the work
+  // group's LDS is released.
+  wait_vmem<0>();
 
   // Epilogue: O = O^T / l, written token-major [N, H, D].
   const float l = lsum + __shfl_xor(lsum, 32);
@@ -695,6 +787,7 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   kp.o_st = a->o_stride_tok; kp.o_sh = a->o_stride_head;
   kp.segs = a->segments; kp.pasts = a->pasts; kp.work = a->work; kp.key_lo = a->key_lo;
   kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
+  kp.num_tokens = a->num_tokens;
   kp.c = a->scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
