@@ -30,8 +30,9 @@
 //                                softmax state; row max/sum need one cross-half
 //                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max is raised lazily (only when it grows by more than kLazyRescale), so
-//   the O accumulators are rarely rescaled.
+//   max is not recomputed per tile, only raised when a tile's row sum shows
+//   that P left fp16's range (kSumLimit), so the O accumulators are rarely
+//   rescaled.
 //   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
 //                                B = P^T straight from the S^T registers: K rows
 //                                are staged in a permuted order that makes the
@@ -49,8 +50,6 @@
 #include <stdint.h>
 #include <stdio.h>
 
-#include <type_traits>
-
 #include "dan_tree_attn.h"
 
 namespace dan {
@@ -59,7 +58,7 @@ constexpr int kKeyTile = DAN_TREE_ATTN_KEY_TILE;  // keys per tile
 constexpr int kWaves = 8;                         // 2 per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWaveQ = 32;                        // queries per wave
-constexpr float kLazyRescale = 8.0f;              // log2 units: p <= 2^8
+constexpr float kSumLimit = 32768.0f;             // per-lane partial row sum of P: keeps p <= 2^15
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -68,6 +67,7 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -82,7 +82,7 @@ struct KParams {
   const DanPastDesc *pasts;
   const DanWorkItem *work;
   const int32_t *key_lo;
-  int32_t num_kv_heads, rep, hpw, chunks, vt_cols, num_tokens;
+  int32_t num_kv_heads, rep, hpw, chunks, vt_cols;
   float c;  // softmax scale * log2(e)
 };
 
@@ -110,8 +110,8 @@ __device__ inline DAN_GLOBAL T *gbl_mut(T *p) {
   return (DAN_GLOBAL T *)p;
 }
 
-// A small table entry at a wave-uniform address, read from global memory
-// dword by dword (the compiler merges the loads) and moved to scalar registers.
+// A small table entry read from global memory (dword by dword; the compiler
+// merges the loads).
 template <typename T>
 __device__ inline T load_entry(const T *p) {
   static_assert(sizeof(T) % 4 == 0, "table entries are dword multiples");
@@ -120,7 +120,7 @@ __device__ inline T load_entry(const T *p) {
   } raw;
   const DAN_GLOBAL uint32_t *src = gbl(reinterpret_cast<const uint32_t *>(p));
 #pragma unroll
-  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = src[i];
   return __builtin_bit_cast(T, raw);
 }
 
@@ -195,6 +195,26 @@ __device__ inline f32x16 mfma32<_Float16>(u32x4 a, u32x4 b, f32x16 c) {
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Dot product of two vectors of 8 16-bit values, accumulated in fp32.
+template <typename TC>
+__device__ inline float dot8(u32x4 a, u32x4 b, float acc);
+template <>
+__device__ inline float dot8<__bf16>(u32x4 a, u32x4 b, float acc) {
+  const bf16x8 x = __builtin_bit_cast(bf16x8, a), y = __builtin_bit_cast(bf16x8, b);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 0, 1), __builtin_shufflevector(y, y, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 2, 3), __builtin_shufflevector(y, y, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 4, 5), __builtin_shufflevector(y, y, 4, 5), acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 6, 7), __builtin_shufflevector(y, y, 6, 7), acc, false);
+}
+template <>
+__device__ inline float dot8<_Float16>(u32x4 a, u32x4 b, float acc) {
+  const f16x8 x = __builtin_bit_cast(f16x8, a), y = __builtin_bit_cast(f16x8, b);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 0, 1), __builtin_shufflevector(y, y, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 2, 3), __builtin_shufflevector(y, y, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 4, 5), __builtin_shufflevector(y, y, 4, 5), acc, false);
+  return __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), __builtin_shufflevector(y, y, 6, 7), acc, false);
+}
+
 // 16-bit element `e` (0..7) of a 16-byte vector, as the low half of a dword.
 __device__ inline uint32_t half_of(u32x4 v, int e) {
   const uint32_t d = v[e >> 1];
@@ -207,13 +227,17 @@ __device__ inline uint32_t half_of(u32x4 v, int e) {
 __device__ inline int k_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 
-// A wave-uniform 64-bit value (pointer or integer), moved to scalar registers.
-template <typename T>
-__device__ inline T uniform64(T x) {
-  static_assert(sizeof(T) == 8, "64-bit values");
-  const uint64_t v = __builtin_bit_cast(uint64_t, x);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+// The value of lane l and of lane l ^ 32 (v_permlane32_swap on a copy). The
+// elements of the result are copied out before the bit casts: clang 22
+// bit-casts an element of an ext_vector by reading element 0.
+struct LanePair {
+  float self, other;
+};
+__device__ inline LanePair lane_pair(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t a = sw[0], b = sw[1];
+  return {__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)};
 }
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone).
@@ -338,21 +362,14 @@ void tree_attn_kernel(const KParams p) {
   const int qend = w.t0 + w.tq;
   const bool wave_work = hig < p.rep && qw0 < qend;
 
-  // K sources in bytes: key coordinate x < P is row x of the prefix-cache
-  // entry, x >= P is token row start + x - P of k. knew0 is where key
-  // coordinate 0 would sit in k's layout (only ever offset to x >= P).
-  const int64_t k_stb = p.k_st * (int64_t)sizeof(TQK);
-  const uint8_t *knew0 = uniform64(reinterpret_cast<const uint8_t *>(static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh) +
-                                   ((int64_t)sg.start - P) * k_stb);
-  const uint8_t *kpast0 = nullptr;
-  int64_t pk_stb = 0;
+  const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
+  const TQK *pkp = nullptr;
+  int64_t pk_st = 0;
   if (P > 0) {
     const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
-    kpast0 = reinterpret_cast<const uint8_t *>(static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head);
-    pk_stb = pd.k_stride_tok * (int64_t)sizeof(TQK);
+    pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
+    pk_st = pd.k_stride_tok;
   }
-  kpast0 = uniform64(kpast0);
-  pk_stb = uniform64(pk_stb);
   const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
 
   // Per-lane query state: lane owns query column lq of its wave. Padding
@@ -369,9 +386,16 @@ void tree_attn_kernel(const KParams p) {
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) qf[kk] = load8<TQK, TQK>(row + 16 * kk);
   }
-
-  const int ntile = w.ja1 + (w.jb1 - w.jb0);
-  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
+  // Raw score of the query against its own key (key coordinate P + query,
+  // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
+  auto self_score = [&](const u32x4(&q)[NK], int qr) __attribute__((always_inline)) {
+    const TQK *krow = kp + (int64_t)qr * p.k_st + 8 * hl;
+    float acc = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) acc = dot8<TQK>(q[kk], load8<TQK, TQK>(krow + 16 * kk), acc);
+    const LanePair lp = lane_pair(acc);
+    return lp.self + lp.other;
+  };
 
   // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
   // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
@@ -383,177 +407,139 @@ void tree_attn_kernel(const KParams p) {
   static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
   const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
   const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
-  // Byte offsets (unsigned 32-bit: the loads take a wave-uniform 64-bit base in
-  // scalar registers plus this per-lane offset).
-  auto k_offset = [&](int blk, int64_t stb) __attribute__((always_inline)) {
+  auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
     const int pos = blk * 64 + lane;
-    return (uint32_t)(k_row(pos / KC) * stb + 8 * min(pos % KC, KC - 2) * (int)sizeof(TQK));
+    return (uint32_t)(k_row(pos / KC) * st + 8 * min(pos % KC, KC - 2));
   };
   auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
     const int pos = blk * 64 + lane;
-    return (uint32_t)(((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2)) * 2);
+    return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
   };
-  // Per-slot offsets: offn is the offset from the tile base (new keys' K or
-  // V^T), offx = offn ^ (past keys' K offset) for K slots and 0 otherwise,
-  // so a past tile takes offn ^ offx without a select between arrays.
-  const bool last_k = last_kind == 0;
-  uint32_t offn[SLOTS], offx[SLOTS];
+  uint32_t kon[KF], kop[KF], von[VF];
 #pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    if (s < KF) {
-      offn[s] = k_offset(wave + kWaves * s, k_stb);
-      offx[s] = offn[s] ^ k_offset(wave + kWaves * s, pk_stb);
-    } else if (s < KF + VF) {
-      offn[s] = v_offset(wave + kWaves * (s - KF));
-      offx[s] = 0;
-    } else if (last_k) {
-      offn[s] = k_offset(last_blk, k_stb);
-      offx[s] = offn[s] ^ k_offset(last_blk, pk_stb);
-    } else {
-      offn[s] = last_kind == 1 ? v_offset(last_blk - L::kInsts) : (uint32_t)((lane & 7) * 16);  // sink: any V^T address
-      offx[s] = 0;
-    }
+  for (int s = 0; s < KF; ++s) {
+    kon[s] = k_offset(wave + kWaves * s, p.k_st);
+    kop[s] = k_offset(wave + kWaves * s, pk_st);
   }
+#pragma unroll
+  for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
+  // last slot: K offsets (new, past) or the V^T / sink offset
+  const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
+  const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
+  const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
 
-  // Direct loads of tile t. On the common path (a whole tile of past keys or
-  // of new keys, inside the batch's rows) the sources are wave-uniform bases
-  // plus the per-lane offsets above, and the slots are issued one at a time
-  // between the matrix instructions of the next step (fire), so the eight
-  // waves do not queue their loads behind the barrier at once. A tile that
-  // straddles the past/new boundary or the end of the batch's rows is issued
-  // at once by prep, per lane; its fire slots, like those of the dummy tiles
-  // past the last one, then load 1 KB of V^T that stays cached into the
-  // sink. Every step thus issues at least SLOTS loads per wave after the
-  // loads of its tile, which is all the vmcnt waits below rely on.
-  struct Tile {
-    const uint8_t *kb, *vb;  // K and V^T tile bases
-    uint32_t pmask;          // ~0: past keys
-    bool dead;               // fire slots are dummies
-  };
-  const uint8_t *vt_u8 = reinterpret_cast<const uint8_t *>(vtp);
-  const uint32_t lane16 = 16 * lane;
-  auto slot_dst = [&](int s, int b, bool dead) __attribute__((always_inline)) {
-    const int blk = s < KF ? wave + kWaves * s : s < KF + VF ? L::kInsts + wave + kWaves * (s - KF) : last_blk;
-    const bool sink = dead || (s == SLOTS - 1 && last_kind == 2);
-    return sink ? smem + L::sink : smem + b * L::buf + blk * 1024;
-  };
-  auto prep = [&](int t) __attribute__((always_inline)) {
-    Tile r;
-    r.kb = r.vb = vt_u8;
-    r.pmask = 0;
-    r.dead = true;
-    if (t < ntile) {
-      const int b = t & 3;
-      const int kb = tile_of(t) * kKeyTile;
-      r.vb = vt_u8 + 2 * kb;
-      if (kb + kKeyTile <= P) {
-        r.kb = kpast0 + kb * pk_stb;
-        r.pmask = ~0u;
-        r.dead = false;
-      } else if (kb >= P && sg.start + kb - P + kKeyTile <= p.num_tokens) {
-        // Rows past the segment's end belong to the next segment; those keys
-        // are after every query of this segment, so the causal mask hides them.
-        r.kb = knew0 + kb * k_stb;
-        r.dead = false;
-      } else {
-        auto k_slow = [&](int blk) __attribute__((always_inline)) {
-          const int pos = blk * 64 + lane;
-          const int col = 8 * min(pos % KC, KC - 2) * (int)sizeof(TQK);
-          const int key = min(kb + k_row(pos / KC), PN - 1);
-          return (key < P ? kpast0 + key * pk_stb : knew0 + key * k_stb) + col;
-        };
+  // Issue the direct loads of key tile j into stage buffer b.
+  auto issue = [&](int j, int b) __attribute__((always_inline)) {
+    const int kb = j * kKeyTile;
+    uint8_t *base = smem + b * L::buf;
+    const _Float16 *vtt = vtp + kb;
+    auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
+      const int pos = blk * 64 + lane;
+      const int col = 8 * min(pos % KC, KC - 2);
+      const int key = min(kb + k_row(pos / KC), PN - 1);
+      return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
+    };
+    // (Separate loops per source layout: a select between two offset arrays
+    // would make the compiler keep them in scratch memory.)
+    if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
+      const TQK *tb = pkp + (int64_t)kb * pk_st;
 #pragma unroll
-        for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), slot_dst(s, b, false));
+      for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
+    } else if (kb >= P && kb + kKeyTile <= PN) {
+      const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
 #pragma unroll
-        for (int s = KF; s < KF + VF; ++s) load_to_lds(r.vb + offn[s], slot_dst(s, b, false));
-        if (last_k) load_to_lds(k_slow(last_blk), slot_dst(SLOTS - 1, b, false));
-        else load_to_lds(r.vb + offn[SLOTS - 1], slot_dst(SLOTS - 1, b, false));
-      }
+      for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
+      if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
     }
-    r.kb = uniform64(r.kb);
-    r.vb = uniform64(r.vb);
-    return r;
-  };
-  auto fire = [&](const Tile &tl, int s, int b) __attribute__((always_inline)) {
-    const bool k = s < KF || (s == SLOTS - 1 && last_k);
-    const uint32_t off = offn[s] ^ (offx[s] & tl.pmask);
-    const uint8_t *src = tl.dead ? vt_u8 + lane16 : (k ? tl.kb : tl.vb) + off;
-    load_to_lds(src, slot_dst(s, b, tl.dead));
+#pragma unroll
+    for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
+    if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
+    if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
   };
 
   f32x16 o[ND];
 #pragma unroll
   for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-  float mrun = -1e30f, lsum = 0.f;
+  // Exponent offset -m of the running max m, which starts at the query's
+  // score against its own key (always visible to it).
+  float mneg = -self_score(qf, qrow) * p.c, lsum = 0.f;
   u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
   // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
-  // Tree mask on boundary tiles (j >= jfull). Key index of register r relative
-  // to the tile start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
-  // sibling-branch gap are per-lane bounds on it: visible iff rel <= lim and
-  // not g0 <= rel < g1 (the gap is empty unless the tile meets [PT, lo_max)).
-  // The mask is applied where S is read (max and exp), never written back, so
-  // S stays in the registers the matrix core wrote.
-  struct Bounds {
-    int lim, g0, g1;
+  auto qk_phase = [&](int b, f32x16(&s)[2]) {
+    const uint8_t *kbuf = smem + b * L::buf;
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
+        s[mb] = mfma32<TQK>(a, qf[kk], s[mb]);
+      }
+    }
   };
-  auto bounds = [&](int j) __attribute__((always_inline)) {
+  // Tree mask on boundary tiles. Key index of register r relative to the tile
+  // start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
+  // sibling-branch gap are per-lane bounds on it; the gap test runs only on
+  // tiles meeting [PT, lo_max).
+  auto mask_phase = [&](int j, f32x16(&s)[2]) {
+    if (j < w.jfull) return;
     const int kb = j * kKeyTile;
-    Bounds m;
-    m.lim = qk - kb - 8 * hl;
-    const bool gap = kb + kKeyTile > PT && kb < w.lo_max;
-    m.g0 = gap ? PT - kb - 8 * hl : 0;
-    m.g1 = gap ? qlo - kb - 8 * hl : 0;
-    return m;
-  };
-  auto vis = [](const Bounds &m, int mb, int r) __attribute__((always_inline)) {
-    const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-    return rel <= m.lim && (rel < m.g0 || rel >= m.g1);
-  };
-  // Running max: raise it (rescaling O and l) only when the tile's max exceeds
-  // it by more than kLazyRescale, so the probabilities stay <= 2^kLazyRescale.
-  // The test needs no cross-lane exchange: a lane holds half of its query's
-  // keys and the other half sits in lane ^ 32 of the same wave, so the
-  // wave-wide vote covers both. Only a rescale combines the two halves, which
-  // keeps the running max identical in both.
-  auto max_phase = [&](const f32x16(&s)[2], bool masked, const Bounds &m) __attribute__((always_inline)) {
-    float x[32];
+    const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
+    if (kb + kKeyTile > PT && kb < w.lo_max) {
+      const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[16 * mb + r] = (!masked || vis(m, mb, r)) ? s[mb][r] : -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+          const bool vis = rel <= lim && (rel < g0 || rel >= g1);
+          s[mb][r] = vis ? s[mb][r] : -INFINITY;
+        }
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+          s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
+        }
+    }
+  };
+  // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
+  // partial row sum of the fp16-rounded values that P V uses (exact products,
+  // fp32 accumulation), so rounding P mostly cancels in O / l. The running
+  // max m starts at tile 0's max and is not recomputed per tile: a partial
+  // row sum above kSumLimit (or inf) means some p left fp16's range or m is
+  // stale by more than log2(kSumLimit / 32); only then is m raised to the
+  // tile's max (O and l rescaled) and the tile's P redone. A lane holds half
+  // of its query's keys and the other half sits in lane ^ 32; both keep the
+  // same m.
+  auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
     float m8[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(x[4 * i], x[4 * i + 1]), fmaxf(x[4 * i + 2], x[4 * i + 3]));
+    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
 #pragma unroll
     for (int w2 = 4; w2 >= 1; w2 >>= 1)
 #pragma unroll
       for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
-    const float mc = m8[0] * p.c;
-    if (__any(mc > mrun + kLazyRescale)) {
-      const float mnew = fmaxf(mrun, fmaxf(mc, __shfl_xor(mc, 32)));
-      const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
-      mrun = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < ND; ++db) o[db] *= alpha;
-    }
+    const LanePair mp = lane_pair(m8[0]);
+    return fmaxf(mp.self, mp.other);
   };
-  // P = exp2(S * c - m) in fp16 (0 where masked); the normalizer sums the
-  // fp16-rounded values that P V uses (exact products, fp32 accumulation), so
-  // rounding P mostly cancels in O / l. (Pairs are taken by shuffling the whole
-  // vector: clang 22 miscompiles __builtin_bit_cast applied to one element of
-  // an ext_vector.)
-  auto exp_phase = [&](const f32x16(&s)[2], bool masked, const Bounds &m) __attribute__((always_inline)) {
-    const float mneg = -mrun;
+  auto exp_phase = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       f32x8 x0, x1;
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const float a0 = fmaf(s[mb][r], p.c, mneg), a1 = fmaf(s[mb][r + 8], p.c, mneg);
-        x0[r] = __builtin_amdgcn_exp2f((!masked || vis(m, mb, r)) ? a0 : -INFINITY);
-        x1[r] = __builtin_amdgcn_exp2f((!masked || vis(m, mb, r + 8)) ? a1 : -INFINITY);
+        x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], p.c, mneg));
+        x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], p.c, mneg));
       }
       pf[2 * mb] = pack8<_Float16>(x0);
       pf[2 * mb + 1] = pack8<_Float16>(x1);
@@ -567,109 +553,81 @@ void tree_attn_kernel(const KParams p) {
       acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc[kj], false);
       acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc[kj], false);
     }
-    lsum += (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
   };
-  f32x16 sc[2];  // S^T of one key tile: 64 keys x this wave's 32 queries
-  // S^T = K Q^T for the 64 keys of stage buffer b (prologue only).
-  auto qk_phase = [&](int b) __attribute__((always_inline)) {
-    const uint8_t *kbuf = smem + b * L::buf;
-    sc[0] = f32x16{};
-    sc[1] = f32x16{};
+  // Accept the tile's P (partial sum ts), raising m to the tile's max (and
+  // redoing P) first if it overflowed.
+  auto finish_tile = [&](const f32x16(&s)[2], float ts) __attribute__((always_inline)) {
+    if (__any(!(ts <= kSumLimit))) {
+      const float mold = -mneg;
+      const float mnew = fmaxf(mold, s_max(s) * p.c);
+      const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+      mneg = -mnew;
+      lsum *= alpha;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
+      for (int db = 0; db < ND; ++db) o[db] *= alpha;
+      ts = exp_phase(s);
+    }
+    lsum += ts;
+  };
+  // O^T += V^T P^T over the 64 keys of stage buffer b.
+  auto pv_phase = [&](int b) __attribute__((always_inline)) {
+    const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
-        sc[mb] = mfma32<TQK>(a, qf[kk], sc[mb]);
+    for (int kj = 0; kj < 4; ++kj) {
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
+        o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
       }
-  };
-  // Matrix phase of step n: S^T(n+1) = K Q^T from stage buffer qb and
-  // O^T += V^T P^T(n) from stage buffer pb, the two MFMA streams interleaved
-  // (six independent accumulator chains), with the direct loads of tile n+3
-  // issued one slot at a time in between. On the last tile S is computed from
-  // a stale but complete buffer and discarded, which keeps the block free of
-  // branches.
-  auto mma_phase = [&](int qb, int pb, const Tile &tl, int fb) __attribute__((always_inline)) {
-    const uint8_t *kbuf = smem + qb * L::buf;
-    const uint8_t *vbuf = smem + pb * L::buf + L::kBytes;
-    constexpr int NQ = 2 * NK, NP = 4 * ND;
-    static_assert(NQ == NP, "QK and PV issue the same number of MFMAs");
-    sc[0] = f32x16{};
-    sc[1] = f32x16{};
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      if (i % 3 == 0 && i / 3 < SLOTS) fire(tl, i / 3, fb);
-      const int kk = i >> 1, mb = i & 1;
-      const u32x4 ka = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
-      sc[mb] = mfma32<TQK>(ka, qf[kk], sc[mb]);
-      const int kj = i / ND, db = i % ND;
-      const u32x4 va = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
-      o[db] = mfma32<_Float16>(va, pf[kj], o[db]);
-    }
-#pragma unroll
-    for (int sl = (NQ + 2) / 3; sl < SLOTS; ++sl) fire(tl, sl, fb);
-    // Schedule: operand reads run two MFMA pairs ahead of their use (enough
-    // to cover LDS latency at one MFMA per 32 cycles, without holding more
-    // than four fragments in registers); each direct load follows the MFMA
-    // pair it was written beside.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads of pairs 0, 1
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      if (i % 3 == 0 && i / 3 < SLOTS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                             // MFMA
-      if (i + 2 < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                            // DS reads
     }
   };
-  // Softmax of tile t (VALU only): running max, then P in fp16.
-  auto softmax = [&](int t) __attribute__((always_inline)) {
-    const int j = tile_of(t);
-    if (j >= w.jfull) {
-      const Bounds m = bounds(j);
-      max_phase(sc, true, m);
-      exp_phase(sc, true, m);
-    } else {
-      max_phase(sc, false, Bounds{});
-      exp_phase(sc, false, Bounds{});
-    }
-  };
+
+  const int ntile = w.ja1 + (w.jb1 - w.jb0);
+  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
   // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
 #pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    const Tile tl = prep(t);
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) fire(tl, s, t);
-  }
-  wait_vmem<2 * SLOTS>();
+  for (int t = 0; t < 3; ++t)
+    if (t < ntile) issue(tile_of(t), t);
+  if (ntile >= 3) wait_vmem<2 * SLOTS>();
+  else if (ntile == 2) wait_vmem<SLOTS>();
+  else wait_vmem<0>();
   barrier_lds();
-  if (ntile > 0) qk_phase(0);
-
-  // Step n (one barrier each): softmax of tile n (VALU), then the matrix
-  // phase M(n) = {S(n+1) = K Q^T, O += V P(n)}. Trailing waves pass the
-  // step's barrier before their softmax, leading waves after it, so on every
-  // SIMD one wave works on the VALU while the other keeps the matrix core
-  // busy.
-  // Stage buffer of tile t is t % 4: the loads of tile n+3 (issued during
-  // M(n), after the barrier) go to the buffer of tile n-1, whose last reader,
-  // M(n-1), precedes the barrier in both wave groups. The wait before the
-  // barrier leaves outstanding only loads issued after tile n+1's.
-  const bool lead = wave < kWaves / 2;  // one leading and one trailing wave per SIMD
-  for (int n = 0; n < ntile; ++n) {
-    if (!lead) {
-      wait_vmem<SLOTS>();
-      barrier_lds();
-    }
-    softmax(n);
-    if (lead) {
-      wait_vmem<SLOTS>();
-      barrier_lds();
-    }
-    const Tile tl = prep(n + 3);
-    mma_phase((n + 1) & 3, n & 3, tl, (n + 3) & 3);
+  f32x16 sa[2], sb[2];
+  if (ntile > 0) {
+    qk_phase(0, sa);
+    mask_phase(tile_of(0), sa);
   }
-  // The trailing steps' loads (into the sink) must land before the work
-  // group's LDS is released.
-  wait_vmem<0>();
+
+  // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
+  // core, then O += V P of tile it while the VALU masks S(it+1).
+  // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
+  // barrier of step it), its buffer's previous tile it-1 is finished by every
+  // wave.
+  int it = 0;
+  auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
+    const bool has_next = it + 1 < ntile;
+    if (has_next) {
+      if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+      else wait_vmem<0>();
+      barrier_lds();
+      if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+    }
+    // S of the next tile is computed unconditionally (on the last tile it
+    // reads a stale but complete buffer and is discarded) so that it shares a
+    // basic block with the softmax VALU work and the two interleave.
+    const float ts = exp_phase(cur);
+    qk_phase((it + 1) & 3, nxt);
+    finish_tile(cur, ts);
+    pv_phase(it & 3);
+    if (has_next) mask_phase(tile_of(it + 1), nxt);
+    ++it;
+  };
+  while (it < ntile) {
+    step(sa, sb);
+    if (it < ntile) step(sb, sa);
+  }
 
   // Epilogue: O = O^T / l, written token-major [N, H, D].
   const float l = lsum + __shfl_xor(lsum, 32);
@@ -787,7 +745,6 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   kp.o_st = a->o_stride_tok; kp.o_sh = a->o_stride_head;
   kp.segs = a->segments; kp.pasts = a->pasts; kp.work = a->work; kp.key_lo = a->key_lo;
   kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
-  kp.num_tokens = a->num_tokens;
   kp.c = a->scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);

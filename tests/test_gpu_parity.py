@@ -116,8 +116,49 @@ def test_single_tokens_and_tiny_segments(gpu):
     check(w, "tiny segments")
 
 
+def _scored_batch(gpu, structure, score_fn, h=8, hkv=2, d=128, seed=0):
+    """Inputs whose raw scores q.k follow score_fn(query_token, key_token):
+    every key row is unit vector u times a per-key coefficient and every
+    query is u times a per-query coefficient, so q.k = a(q) b(k) exactly; v
+    is random. Packed one segment after another from ``structure``."""
+    rng = np.random.default_rng(seed)
+    n = sum(t + sum(ls) for t, ls in structure)
+    u = rng.standard_normal(d).astype(np.float32)
+    u /= np.linalg.norm(u)
+    a, b = score_fn(np.arange(n))
+    q = np.broadcast_to((a[:, None, None] * u), (n, h, d)).copy()
+    k = np.broadcast_to((b[:, None, None] * u), (n, hkv, d)).copy()
+    v = rng.standard_normal((n, hkv, d), dtype=np.float32)
+    to = lambda x: torch.from_numpy(x).to(torch.float32).to(gpu).transpose(0, 1)
+    segs, start = Batch(), 0
+    for trunk, lens in structure:
+        ids = W.branch_ids(trunk, lens)
+        segs.append(segment(start, ids, None, 0, 0, gpu))
+        start += len(ids)
+    return W.Workload("scored", to(q), to(k), to(v), segs, 0, {})
+
+
+def test_running_max_set_by_first_visible_key(gpu):
+    """Empty trunk, two branches; the second branch's queries share a work
+    item with the first branch's tail but see none of key tile 0. All scores
+    are near -300 / sqrt(D) * log2 e below zero, so a running max left at 0
+    would underflow every probability."""
+    w = _scored_batch(gpu, [(0, [80, 70])], lambda t: (np.full(t.shape, -20.0, np.float32),
+                                                          np.full(t.shape, 15.0, np.float32) + 0.01 * t))
+    check(w, "negative scores, first visible key after tile 0")
+
+
+def test_running_max_raised_by_growing_scores(gpu):
+    """Scores grow with the key index along a 1000-token trunk, so later
+    tiles keep exceeding the running max: the rescale path runs on most
+    tiles."""
+    w = _scored_batch(gpu, [(1000, [40, 24])], lambda t: (np.full(t.shape, 4.0, np.float32),
+                                                          0.1 * t.astype(np.float32)))
+    check(w, "growing scores")
+
+
 def test_fp32_config1_layout(gpu):
-    """fp32 in, fp32 out (staged to bf16 for the matrix cores)."""
+    """fp32 in, fp32 out (staged through fp16 for the matrix cores)."""
     out, _ = check(W.config1(1, device=gpu), "c1 seed 1")
     assert out.dtype == torch.float32
 
