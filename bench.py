@@ -36,17 +36,19 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def useful_flops(w):
-    from oracle.tree_attention import useful_pairs  # same closed form for GPU and CPU
+    from dan_amd.workloads import useful_pairs
 
     return 4 * w.q.shape[2] * w.q.shape[0] * useful_pairs(w.segments)
 
 
 def algorithmic_bytes(w):
-    """Q + K + V + O once, plus each distinct past tensor once."""
+    """Q + K + V read once, O written once (bf16 for e4m3 inputs), plus each
+    distinct past tensor once."""
     h, n, d = w.q.shape
     hkv = w.k.shape[0]
     es = w.q.element_size()
-    total = (2 * n * h * d + 2 * n * hkv * d) * es
+    es_out = 2 if w.q.dtype == torch.float8_e4m3fn else es
+    total = (n * h * d + 2 * n * hkv * d) * es + n * h * d * es_out
     seen = set()
     for s in w.segments:
         if s.past and id(s.past) not in seen:
@@ -74,6 +76,8 @@ def cpu_baseline(name, seed, flops, n_tokens):
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
+    if name == "c5":  # e4m3 inputs: the CPU path runs on config 3's originals (same useful FLOPs)
+        name = "c3"
     w = workloads.CONFIGS[name](seed, device="cpu")
     attend_dense(w.q, w.k, w.v, w.segments, w.layer)
     times = []
@@ -105,7 +109,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -133,11 +137,13 @@ def main():
     flops = useful_flops(w)
     nbytes = algorithmic_bytes(w)
     n = w.num_tokens
-    dtype = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[w.q.dtype]
+    dtype = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32",
+             torch.float8_e4m3fn: "fp8"}[w.q.dtype]
+    kw = w.attend_kwargs
 
     out = None
     for _ in range(args.warmup):
-        out = attend(w.q, w.k, w.v, w.segments, w.layer)
+        out = attend(w.q, w.k, w.v, w.segments, w.layer, **kw)
     torch.cuda.synchronize()
     if out is not None and not torch.isfinite(out).all():
         raise RuntimeError("non-finite output")
@@ -149,7 +155,7 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         starts[i].record(stream)
-        attend(w.q, w.k, w.v, w.segments, w.layer)
+        attend(w.q, w.k, w.v, w.segments, w.layer, **kw)
         ends[i].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -182,13 +188,15 @@ def main():
         "config": {"workload": f"{args.workload}: " + (workloads.CONFIGS[args.workload].__doc__ or "").split(";")[0]
                    .strip().replace("\n", " "),
                    "seed": args.seed, "packed_tokens": n, "heads": f"{w.q.shape[0]}/{w.k.shape[0]}",
-                   "head_dim": w.q.shape[2], **{k: v for k, v in w.meta.items() if k != "packed_tokens"},
+                   "head_dim": w.q.shape[2],
+                   **{k: v for k, v in w.meta.items() if k != "packed_tokens" and not isinstance(v, torch.Tensor)},
                    "useful_gflop": round(flops / 1e9, 3), "algorithmic_mb": round(nbytes / 1e6, 2)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic,
                      "kernel_ms_avg": round(k_avg, 4), "kernel_ms_median": round(k_med, 4),
                      "hbm_gbps_algorithmic": round(nbytes / (k_avg * 1e-3) / 1e9, 1),
-                     "hbm_frac_algorithmic": round(nbytes / (k_avg * 1e-3) / 1e9 / HBM_GBPS, 4)},
+                     "hbm_frac_algorithmic": round(nbytes / (k_avg * 1e-3) / 1e9 / HBM_GBPS, 4),
+                     "bf16_peak_frac": round(achieved / PEAK_TFLOPS["bf16"], 4)},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

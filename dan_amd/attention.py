@@ -123,10 +123,12 @@ def repeat_heads(x, rep):
     return x[:, :, None].expand(n, h, rep, d).reshape(n, h * rep, d)
 
 
-_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_F16, torch.float32: _native.DTYPE_F32}
+E4M3 = torch.float8_e4m3fn
+_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_F16, torch.float32: _native.DTYPE_F32,
+           E4M3: _native.DTYPE_E4M3}
 
 
-def attend(q, k, v, segments, layer, scale=None):
+def attend(q, k, v, segments, layer, scale=None, *, q_scale=None, k_scale=None, v_scale=None):
     """q: [H, N, D]; k, v: [Hkv, N, D] (rotary applied). Returns [H, N, D]
     (dan/attention.py:200-207).
 
@@ -134,11 +136,20 @@ def attend(q, k, v, segments, layer, scale=None):
     ``saved[layer] = (k[:, start:start+save].clone(), v[...].clone())``.
     The result is a [H, N, D] view of token-major [N, H, D] storage, so the
     caller's ``o.transpose(0, 1).reshape(n, H * D)`` needs no copy. Rows not
-    covered by any segment are left uninitialized, as in the reference."""
+    covered by any segment are left uninitialized, as in the reference.
+
+    FP8: q, k, v of dtype ``torch.float8_e4m3fn`` quantized per tensor as in
+    dan/fused.py:85-91 and dan/quant.py:28-31 (x ~ xq * scale), with their
+    fp32 scales in ``q_scale``, ``k_scale``, ``v_scale`` (one-element device
+    tensors). The output is bf16. An e4m3 prefix-cache entry is
+    ``past[layer] = (k, v, k_scale, v_scale)``; a saving segment keeps the
+    same four-tuple."""
+    fp8 = q.dtype == E4M3
     for s in segments:
         if s.save:
-            s.saved[layer] = (k[:, s.start:s.start + s.save].clone(), v[:, s.start:s.start + s.save].clone())
-    return _attend_fused(q, k, v, segments, layer, scale)
+            kv = (k[:, s.start:s.start + s.save].clone(), v[:, s.start:s.start + s.save].clone())
+            s.saved[layer] = kv + (k_scale.clone(), v_scale.clone()) if fp8 and k_scale is not None else kv
+    return _attend_fused(q, k, v, segments, layer, scale, (q_scale, k_scale, v_scale) if fp8 else None)
 
 
 def _check_inputs(q, k, v):
@@ -156,6 +167,12 @@ def _check_inputs(q, k, v):
         raise ValueError(f"head_dim {d}: the gfx950 kernel is built for 64 and 128")
     if not (q.device == k.device == v.device):
         raise ValueError("q, k, v must be on one device")
+
+
+def _check_scale(t, name, device):
+    if not (isinstance(t, torch.Tensor) and t.numel() == 1 and t.dtype == torch.float32 and t.device == device):
+        raise ValueError(f"e4m3 inputs need {name}: a one-element fp32 tensor on {device}")
+    return t.reshape(1).contiguous()
 
 
 def _aligned(t):
@@ -189,7 +206,8 @@ def _qk_dtype(dtype):
 
 
 def _past_table(plan, layer, hkv, d, dtype, device):
-    """Device table of DanPastDesc for ``layer`` (cached on the plan)."""
+    """Device table of DanPastDesc for ``layer`` (cached on the plan). An
+    e4m3 entry is (k, v, k_scale, v_scale)."""
     hit = plan.past_tables.get(layer)
     if hit is not None:
         return hit
@@ -197,7 +215,16 @@ def _past_table(plan, layer, hkv, d, dtype, device):
     descs = (_native.DanPastDesc * max(n, 1))()
     refs = []
     for i, past in enumerate(plan.past_dicts):
-        pk, pv = past[layer]
+        entry = past[layer]
+        if dtype == E4M3:
+            if len(entry) != 4:
+                raise ValueError(f"past entry {i}, layer {layer}: e4m3 entries are (k, v, k_scale, v_scale)")
+            pk, pv = entry[:2]
+            pks, pvs = _check_scale(entry[2], "the past k_scale", device), _check_scale(entry[3], "the past v_scale", device)
+            refs += [pks, pvs]
+            descs[i].k_scale, descs[i].v_scale = pks.data_ptr(), pvs.data_ptr()
+        else:
+            pk, pv = entry[:2]
         plen = pk.shape[1] if pk.dim() == 3 else -1
         want = (hkv, plen, d)
         if pk.dim() != 3 or tuple(pk.shape) != want or tuple(pv.shape) != want:
@@ -228,7 +255,7 @@ def _workspace(plan, nbytes, device):
     return ws
 
 
-def _attend_fused(q, k, v, segments, layer, scale):
+def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None):
     if not q.is_cuda:
         raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
                            f"{q.device} (the masked CPU path is the test oracle, not a backend)")
@@ -245,7 +272,9 @@ def _attend_fused(q, k, v, segments, layer, scale):
         raise ValueError(f"unsupported head layout H={h}, Hkv={hkv}")
     plan = get_plan(segments, n, tile_q, q.device)
     table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
-    out_dtype = q.dtype
+    out_dtype = torch.bfloat16 if q.dtype == E4M3 else q.dtype
+    if q.dtype == E4M3:
+        q_scale, k_scale, v_scale = (_check_scale(t, nm, q.device) for t, nm in zip(fp8_scales, ("q_scale", "k_scale", "v_scale")))
     qk_dtype = _qk_dtype(q.dtype)
     q, k, v = _kernel_view(q.to(qk_dtype)), _kernel_view(k.to(qk_dtype)), _kernel_view(v)
     out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
@@ -271,5 +300,7 @@ def _attend_fused(q, k, v, segments, layer, scale):
         a.vt_cols = plan.vt_cols
         a.col_seg = plan.col_seg_d.data_ptr()
         a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+        if q.dtype == E4M3:
+            a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

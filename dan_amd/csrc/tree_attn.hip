@@ -72,6 +72,30 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 constexpr f16x2 kOnes2 = {(_Float16)1.0f, (_Float16)1.0f};
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+
+// OCP float8 e4m3fn (the format of torch.float8_e4m3fn), as stored.
+struct E4M3 {
+  uint8_t bits;
+};
+
+// Operand traits of S = K Q^T on the matrix core. A lane's fragment of one
+// k-step is `chunks` 16-byte pieces: 8 values of a 16-bit type
+// (v_mfma_f32_32x32x16_{bf16,f16}, k-step 16) or 32 e4m3 values
+// (v_mfma_f32_32x32x64_f8f6f4, k-step 64). Lane l holds row l % 32 and the
+// k-range [step/2 * (l / 32), +step/2) of the step.
+template <typename T>
+struct QK {
+  static constexpr int step = 16, chunks = 1;
+};
+template <>
+struct QK<E4M3> {
+  static constexpr int step = 64, chunks = 2;
+};
+template <typename T>
+struct Frag {
+  u32x4 c[QK<T>::chunks];
+};
 
 struct KParams {
   const void *q, *k;
@@ -84,6 +108,9 @@ struct KParams {
   const int32_t *key_lo;
   int32_t num_kv_heads, rep, hpw, chunks, vt_cols;
   float c;  // softmax scale * log2(e)
+  // e4m3 only: per-tensor scales of q and k (device fp32 scalars); S is
+  // scaled by q_scale * k_scale (a prefix-cache entry has its own k scale).
+  const float *q_scale, *k_scale;
 };
 
 struct PackParams {
@@ -94,6 +121,7 @@ struct PackParams {
   const int32_t *col_seg;
   _Float16 *vt;
   int32_t num_kv_heads, vt_cols;
+  const float *v_scale;  // e4m3 only: per-tensor scale of v (prefix-cache entries carry their own)
 };
 
 // ---------------------------------------------------------------- element I/O
@@ -156,6 +184,31 @@ __device__ inline u32x4 load8<__bf16, _Float16>(const __bf16 *p) {
   return __builtin_bit_cast(u32x4, __builtin_convertvector(x, f16x8));
 }
 
+// 8 e4m3 values (8 bytes) -> 8 fp32 values.
+__device__ inline f32x8 e4m3x8_to_f32(u32x2 v) {
+  f32x8 x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(v[i], false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(v[i], true);
+    const float a = lo[0], b = lo[1], c = hi[0], d = hi[1];
+    x[4 * i] = a;
+    x[4 * i + 1] = b;
+    x[4 * i + 2] = c;
+    x[4 * i + 3] = d;
+  }
+  return x;
+}
+
+// A lane's operand fragment of one k-step: `chunks` consecutive 16-byte
+// pieces starting at p.
+template <typename T>
+__device__ inline Frag<T> load_frag(const T *p) {
+  Frag<T> f;
+#pragma unroll
+  for (int i = 0; i < QK<T>::chunks; ++i) f.c[i] = *gbl(reinterpret_cast<const u32x4 *>(p) + i);
+  return f;
+}
+
 template <typename TC>
 __device__ inline u32x4 pack8(f32x8 x);
 template <>
@@ -215,6 +268,33 @@ __device__ inline float dot8<_Float16>(u32x4 a, u32x4 b, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), __builtin_shufflevector(y, y, 6, 7), acc, false);
 }
 
+template <typename T>
+__device__ inline f32x16 mfma_qk(const Frag<T> &a, const Frag<T> &b, f32x16 c) {
+  return mfma32<T>(a.c[0], b.c[0], c);
+}
+template <>
+__device__ inline f32x16 mfma_qk<E4M3>(const Frag<E4M3> &a, const Frag<E4M3> &b, f32x16 c) {
+  const i32x8 x = __builtin_bit_cast(i32x8, a), y = __builtin_bit_cast(i32x8, b);
+  // Format codes 0, 0: both operands OCP e4m3; no block scales.
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x, y, c, 0, 0, 0, 0, 0, 0);
+}
+template <typename T>
+__device__ inline float dot_frag(const Frag<T> &a, const Frag<T> &b, float acc) {
+  return dot8<T>(a.c[0], b.c[0], acc);
+}
+template <>
+__device__ inline float dot_frag<E4M3>(const Frag<E4M3> &a, const Frag<E4M3> &b, float acc) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const u32x4 x4 = a.c[i], y4 = b.c[i];
+    const u32x2 xl = {x4[0], x4[1]}, xh = {x4[2], x4[3]}, yl = {y4[0], y4[1]}, yh = {y4[2], y4[3]};
+    const f32x8 x0 = e4m3x8_to_f32(xl), x1 = e4m3x8_to_f32(xh), y0 = e4m3x8_to_f32(yl), y1 = e4m3x8_to_f32(yh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = fmaf(x0[j], y0[j], fmaf(x1[j], y1[j], acc));
+  }
+  return acc;
+}
+
 // 16-bit element `e` (0..7) of a 16-byte vector, as the low half of a dword.
 __device__ inline uint32_t half_of(u32x4 v, int e) {
   const uint32_t d = v[e >> 1];
@@ -268,9 +348,9 @@ __device__ inline void load_to_lds(const T *src, uint8_t *lds) {
 // chunks, V^T: D * 9 chunks); the pad chunks receive a duplicate of the row's
 // last chunk. A 1 KB sink after the buffers absorbs the direct-load slots that
 // round the per-wave load count up to a constant.
-template <int D>
+template <int D, int KB = 2>  // KB: bytes per K element
 struct Lds {
-  static constexpr int kChunks = D / 8 + 1;
+  static constexpr int kChunks = D * KB / 16 + 1;
   static constexpr int kRow = kChunks * 16;
   static constexpr int kBytes = kKeyTile * kRow;
   static constexpr int kInsts = kKeyTile * kChunks / 64;
@@ -291,8 +371,20 @@ struct Lds {
 // keys of the block (past rows from the segment's prefix-cache entry, new rows
 // from v; zero past the segment's end), converts them to fp16 and writes them
 // transposed, 128 contiguous bytes per d.
+// 8 consecutive values of v times `scale` (e4m3 only) -> 8 fp16 values.
+template <typename TV>
+__device__ inline u32x4 load8_v(const TV *p, float) {
+  return load8<TV, _Float16>(p);
+}
+template <>
+__device__ inline u32x4 load8_v<E4M3>(const E4M3 *p, float scale) {
+  const f32x8 x = e4m3x8_to_f32(*gbl(reinterpret_cast<const u32x2 *>(p))) * scale;
+  return __builtin_bit_cast(u32x4, __builtin_convertvector(x, f16x8));
+}
+
 template <typename TV, int D>
 __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
+  constexpr bool kF8 = std::is_same<TV, E4M3>::value;
   constexpr int CPR = D / 8;
   constexpr int KPP = 256 / CPR;  // keys per load pass
   __shared__ __attribute__((aligned(16))) uint16_t tile[D][kKeyTile + 8];
@@ -303,10 +395,13 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   const TV *vp = static_cast<const TV *>(p.v) + (int64_t)kvh * p.v_sh;
   const TV *pvp = nullptr;
   int64_t pv_st = 0;
+  float vs = 1.f, pvs = 1.f;
+  if (kF8) vs = *gbl(p.v_scale);
   if (P > 0) {
     const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
     pvp = static_cast<const TV *>(pd.v) + (int64_t)kvh * pd.v_stride_head;
     pv_st = pd.v_stride_tok;
+    if (kF8) pvs = *gbl(pd.v_scale);
   }
   const int c = threadIdx.x % CPR;
 #pragma unroll
@@ -315,8 +410,8 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     const int key = key0 + kr;
     u32x4 x = {0, 0, 0, 0};
     if (key < PN)
-      x = load8<TV, _Float16>(key < P ? pvp + (int64_t)key * pv_st + 8 * c
-                                      : vp + (int64_t)(sg.start + key - P) * p.v_st + 8 * c);
+      x = key < P ? load8_v<TV>(pvp + (int64_t)key * pv_st + 8 * c, pvs)
+                  : load8_v<TV>(vp + (int64_t)(sg.start + key - P) * p.v_st + 8 * c, vs);
 #pragma unroll
     for (int e = 0; e < 8; ++e) tile[8 * c + e][kr] = (uint16_t)half_of(x, e);
   }
@@ -330,14 +425,17 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
 }
 
 // ---------------------------------------------------------------- attention
-// TQK: matrix-core type of S = K Q^T (q, k and the pasts' k). P V always runs
-// in fp16: P in [0, 2^8] keeps 11 significant bits instead of bf16's 8, and
-// the V^T copy is fp16.
+// TQK: matrix-core type of S = K Q^T (q, k and the pasts' k): bf16, fp16 or
+// e4m3. P V always runs in fp16: P keeps 11 significant bits instead of
+// bf16's 8 (or e4m3's 4), and the V^T copy is fp16.
 template <typename TQK, typename TOut, int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
 void tree_attn_kernel(const KParams p) {
-  using L = Lds<D>;
-  constexpr int NK = D / 16;   // k-steps of Q K^T
+  using L = Lds<D, (int)sizeof(TQK)>;
+  constexpr bool kF8 = std::is_same<TQK, E4M3>::value;
+  constexpr int KS = QK<TQK>::step;                   // k-step of Q K^T
+  constexpr int NK = D / KS;                          // k-steps of Q K^T
+  constexpr int CE = 16 / (int)sizeof(TQK);           // K / Q elements per 16-byte chunk
   constexpr int ND = D / 32;   // 32-row d blocks of O^T
   constexpr int SLOTS = L::slots;
   constexpr int KC = L::kChunks;
@@ -365,10 +463,15 @@ void tree_attn_kernel(const KParams p) {
   const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
   const TQK *pkp = nullptr;
   int64_t pk_st = 0;
+  // Softmax exponent factor c of S: scale * log2(e), times q_scale * k_scale
+  // for e4m3 (the prefix-cache entry's k has its own scale, c_past).
+  float c_new = p.c, c_past = p.c;
+  if (kF8) c_new = c_past = p.c * *gbl(p.q_scale) * *gbl(p.k_scale);
   if (P > 0) {
     const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
     pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
     pk_st = pd.k_stride_tok;
+    if (kF8) c_past = p.c * *gbl(p.q_scale) * *gbl(pd.k_scale);
   }
   const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
 
@@ -380,19 +483,19 @@ void tree_attn_kernel(const KParams p) {
   const int qrow = sg.start + min(ql, qend - 1);
   const int qk = qvalid ? P + ql : 0x3fffffff;
   const int qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
-  u32x4 qf[NK];
+  Frag<TQK> qf[NK];
   {
-    const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + 8 * hl;
+    const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) qf[kk] = load8<TQK, TQK>(row + 16 * kk);
+    for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
   }
   // Raw score of the query against its own key (key coordinate P + query,
   // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
-  auto self_score = [&](const u32x4(&q)[NK], int qr) __attribute__((always_inline)) {
-    const TQK *krow = kp + (int64_t)qr * p.k_st + 8 * hl;
+  auto self_score = [&](const Frag<TQK>(&q)[NK], int qr) __attribute__((always_inline)) {
+    const TQK *krow = kp + (int64_t)qr * p.k_st + KS / 2 * hl;
     float acc = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) acc = dot8<TQK>(q[kk], load8<TQK, TQK>(krow + 16 * kk), acc);
+    for (int kk = 0; kk < NK; ++kk) acc = dot_frag<TQK>(q[kk], load_frag<TQK>(krow + KS * kk), acc);
     const LanePair lp = lane_pair(acc);
     return lp.self + lp.other;
   };
@@ -409,13 +512,13 @@ void tree_attn_kernel(const KParams p) {
   const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
   auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
     const int pos = blk * 64 + lane;
-    return (uint32_t)(k_row(pos / KC) * st + 8 * min(pos % KC, KC - 2));
+    return (uint32_t)(k_row(pos / KC) * st + CE * min(pos % KC, KC - 2));
   };
   auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
     const int pos = blk * 64 + lane;
     return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
   };
-  uint32_t kon[KF], kop[KF], von[VF];
+  uint32_t kon[KF > 0 ? KF : 1], kop[KF > 0 ? KF : 1], von[VF > 0 ? VF : 1];  // (KF is 0 for e4m3, D = 64)
 #pragma unroll
   for (int s = 0; s < KF; ++s) {
     kon[s] = k_offset(wave + kWaves * s, p.k_st);
@@ -435,7 +538,7 @@ void tree_attn_kernel(const KParams p) {
     const _Float16 *vtt = vtp + kb;
     auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
       const int pos = blk * 64 + lane;
-      const int col = 8 * min(pos % KC, KC - 2);
+      const int col = CE * min(pos % KC, KC - 2);
       const int key = min(kb + k_row(pos / KC), PN - 1);
       return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
     };
@@ -467,7 +570,7 @@ void tree_attn_kernel(const KParams p) {
   for (int db = 0; db < ND; ++db) o[db] = f32x16{};
   // Exponent offset -m of the running max m, which starts at the query's
   // score against its own key (always visible to it).
-  float mneg = -self_score(qf, qrow) * p.c, lsum = 0.f;
+  float mneg = -self_score(qf, qrow) * c_new, lsum = 0.f;
   u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
   // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
@@ -479,8 +582,12 @@ void tree_attn_kernel(const KParams p) {
     for (int kk = 0; kk < NK; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow + (2 * kk + hl) * 16);
-        s[mb] = mfma32<TQK>(a, qf[kk], s[mb]);
+        Frag<TQK> a;
+#pragma unroll
+        for (int i = 0; i < QK<TQK>::chunks; ++i)
+          a.c[i] = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow +
+                                                    ((2 * kk + hl) * QK<TQK>::chunks + i) * 16);
+        s[mb] = mfma_qk<TQK>(a, qf[kk], s[mb]);
       }
     }
   };
@@ -512,6 +619,23 @@ void tree_attn_kernel(const KParams p) {
         }
     }
   };
+  // Exponent factor of tile j's scores, and (e4m3) the fix-up of a tile that
+  // holds both prefix-cache and new keys: the prefix keys' scores are brought
+  // to the new keys' k scale, and the tile then uses c_new.
+  auto tile_c = [&](int j) __attribute__((always_inline)) { return j * kKeyTile + kKeyTile <= P ? c_past : c_new; };
+  auto fix_straddle = [&](int j, f32x16(&s)[2]) __attribute__((always_inline)) {
+    const int kb = j * kKeyTile;
+    if (!kF8 || !(kb < P && kb + kKeyTile > P)) return;
+    const float ratio = c_past / c_new;
+    const int lim = P - kb - 8 * hl;  // prefix key: rel < lim
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+        s[mb][r] = rel < lim ? s[mb][r] * ratio : s[mb][r];
+      }
+  };
   // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
   // partial row sum of the fp16-rounded values that P V uses (exact products,
   // fp32 accumulation), so rounding P mostly cancels in O / l. The running
@@ -532,14 +656,14 @@ void tree_attn_kernel(const KParams p) {
     const LanePair mp = lane_pair(m8[0]);
     return fmaxf(mp.self, mp.other);
   };
-  auto exp_phase = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {
+  auto exp_phase = [&](const f32x16(&s)[2], float c) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       f32x8 x0, x1;
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], p.c, mneg));
-        x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], p.c, mneg));
+        x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], c, mneg));
+        x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], c, mneg));
       }
       pf[2 * mb] = pack8<_Float16>(x0);
       pf[2 * mb + 1] = pack8<_Float16>(x1);
@@ -557,16 +681,16 @@ void tree_attn_kernel(const KParams p) {
   };
   // Accept the tile's P (partial sum ts), raising m to the tile's max (and
   // redoing P) first if it overflowed.
-  auto finish_tile = [&](const f32x16(&s)[2], float ts) __attribute__((always_inline)) {
+  auto finish_tile = [&](const f32x16(&s)[2], float ts, float c) __attribute__((always_inline)) {
     if (__any(!(ts <= kSumLimit))) {
       const float mold = -mneg;
-      const float mnew = fmaxf(mold, s_max(s) * p.c);
+      const float mnew = fmaxf(mold, s_max(s) * c);
       const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
       mneg = -mnew;
       lsum *= alpha;
 #pragma unroll
       for (int db = 0; db < ND; ++db) o[db] *= alpha;
-      ts = exp_phase(s);
+      ts = exp_phase(s, c);
     }
     lsum += ts;
   };
@@ -598,6 +722,7 @@ void tree_attn_kernel(const KParams p) {
   if (ntile > 0) {
     qk_phase(0, sa);
     mask_phase(tile_of(0), sa);
+    fix_straddle(tile_of(0), sa);
   }
 
   // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
@@ -617,11 +742,15 @@ void tree_attn_kernel(const KParams p) {
     // S of the next tile is computed unconditionally (on the last tile it
     // reads a stale but complete buffer and is discarded) so that it shares a
     // basic block with the softmax VALU work and the two interleave.
-    const float ts = exp_phase(cur);
+    const float c = tile_c(tile_of(it));
+    const float ts = exp_phase(cur, c);
     qk_phase((it + 1) & 3, nxt);
-    finish_tile(cur, ts);
+    finish_tile(cur, ts, c);
     pv_phase(it & 3);
-    if (has_next) mask_phase(tile_of(it + 1), nxt);
+    if (has_next) {
+      mask_phase(tile_of(it + 1), nxt);
+      fix_straddle(tile_of(it + 1), nxt);
+    }
     ++it;
   };
   while (it < ntile) {
@@ -668,10 +797,11 @@ hipError_t launch_pack(const PackParams &pp, int blocks, hipStream_t stream) {
 template <typename TQK, typename TOut, int D>
 hipError_t launch_attn(const KParams &kp, int grid, hipStream_t stream) {
   auto kernel = tree_attn_kernel<TQK, TOut, D>;
+  constexpr int lds = Lds<D, (int)sizeof(TQK)>::total;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::total);
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), Lds<D>::total, stream, kp);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, kp);
   return hipGetLastError();
 }
 
@@ -710,7 +840,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   const bool bf16 = in == DAN_DTYPE_BF16 && vd == DAN_DTYPE_BF16 && out == DAN_DTYPE_BF16;
   const bool f16 = in == DAN_DTYPE_F16 && vd == DAN_DTYPE_F16 && out == DAN_DTYPE_F16;
   const bool f32 = in == DAN_DTYPE_F16 && vd == DAN_DTYPE_F32 && out == DAN_DTYPE_F32;
-  if (!bf16 && !f16 && !f32)
+  const bool f8 = in == DAN_DTYPE_E4M3 && vd == DAN_DTYPE_E4M3 && out == DAN_DTYPE_BF16;
+  if (!bf16 && !f16 && !f32 && !f8)
     return fail(DAN_ERR_UNSUPPORTED, "dtype combination q/k=%d v=%d out=%d is not built", in, vd, out);
   if (a->num_work < 0 || a->num_segments < 0 || a->num_pasts < 0 || a->num_tokens < 0 || a->vt_cols < 0)
     return fail(DAN_ERR_INVALID_ARGUMENT, "negative count");
@@ -718,6 +849,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   if (!a->q || !a->k || !a->v || !a->out || !a->segments || !a->work || !a->key_lo || !a->col_seg)
     return fail(DAN_ERR_INVALID_ARGUMENT, "NULL tensor or table pointer");
   if (a->num_pasts > 0 && !a->pasts) return fail(DAN_ERR_INVALID_ARGUMENT, "num_pasts > 0 with NULL pasts");
+  if (f8 && (!a->q_scale || !a->k_scale || !a->v_scale))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "e4m3 inputs need q_scale, k_scale and v_scale");
   if (!(a->scale > 0.f) || !isfinite(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
   const int64_t need = dan_tree_attn_workspace_size(Hkv, D, a->vt_cols);
   if (a->vt_cols <= 0 || need <= 0) return fail(DAN_ERR_INVALID_ARGUMENT, "vt_cols %d must be a positive multiple of %d", a->vt_cols, kKeyTile);
@@ -737,6 +870,7 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   pp.segs = a->segments; pp.pasts = a->pasts; pp.col_seg = a->col_seg;
   pp.vt = static_cast<_Float16 *>(a->workspace);
   pp.num_kv_heads = Hkv; pp.vt_cols = a->vt_cols;
+  pp.v_scale = a->v_scale;
 
   KParams kp;
   kp.q = a->q; kp.k = a->k; kp.o = a->out; kp.vt = pp.vt;
@@ -746,17 +880,20 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   kp.segs = a->segments; kp.pasts = a->pasts; kp.work = a->work; kp.key_lo = a->key_lo;
   kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
   kp.c = a->scale * 1.4426950408889634f;
+  kp.q_scale = a->q_scale; kp.k_scale = a->k_scale;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool d128 = D == 128;
   hipError_t err;
   if (bf16) err = d128 ? launch_pack<__bf16, 128>(pp, (int)pack_grid, s) : launch_pack<__bf16, 64>(pp, (int)pack_grid, s);
   else if (f16) err = d128 ? launch_pack<_Float16, 128>(pp, (int)pack_grid, s) : launch_pack<_Float16, 64>(pp, (int)pack_grid, s);
+  else if (f8) err = d128 ? launch_pack<E4M3, 128>(pp, (int)pack_grid, s) : launch_pack<E4M3, 64>(pp, (int)pack_grid, s);
   else err = d128 ? launch_pack<float, 128>(pp, (int)pack_grid, s) : launch_pack<float, 64>(pp, (int)pack_grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "V^T pack launch failed: %s", hipGetErrorString(err));
 
   if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, (int)grid, s) : launch_attn<__bf16, __bf16, 64>(kp, (int)grid, s);
   else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, (int)grid, s) : launch_attn<_Float16, _Float16, 64>(kp, (int)grid, s);
+  else if (f8) err = d128 ? launch_attn<E4M3, __bf16, 128>(kp, (int)grid, s) : launch_attn<E4M3, __bf16, 64>(kp, (int)grid, s);
   else err = d128 ? launch_attn<_Float16, float, 128>(kp, (int)grid, s) : launch_attn<_Float16, float, 64>(kp, (int)grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
   return DAN_OK;

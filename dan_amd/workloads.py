@@ -11,7 +11,7 @@ q, k, v are laid out as the Llama attention module hands them to ``attend``
 token-major fused projection buffer [N, H + 2 Hkv, D].
 """
 import hashlib
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 import torch
@@ -35,6 +35,11 @@ class Workload:
     @property
     def num_tokens(self):
         return self.q.shape[1]
+
+    @property
+    def attend_kwargs(self):
+        """Extra arguments of ``attend`` for this workload (the e4m3 scales)."""
+        return {k: self.meta[k] for k in ("q_scale", "k_scale", "v_scale") if k in self.meta}
 
     def digest(self):
         """SHA-256 over q, k, v and every distinct past tensor (raw bytes)."""
@@ -176,6 +181,62 @@ def config4(seed=0, device="cpu"):
                  **LLAMA3_8B)
 
 
+def useful_pairs(segments):
+    """Visible (query, key) pairs of a batch, counted per query: query i of a
+    segment sees its p + i + 1 causal keys except, for a branch query, the
+    sibling span between the trunk's end (p + trunk) and its own branch's
+    start. Useful FLOPs are 4 * head_dim * num_heads * pairs (QK^T and PV)."""
+    total = 0
+    for s in segments:
+        p = s.past_len if s.past else 0
+        n = s.end - s.start
+        lo = np.zeros(n, np.int64)
+        for a, b in s.branches:
+            lo[a - s.start:b - s.start] = p + (a - s.start)
+        gap = np.maximum(lo - (p + s.trunk), 0)
+        total += int((p + np.arange(n) + 1 - gap).sum())
+    return total
+
+
+E4M3_MAX = 448.0  # torch.finfo(torch.float8_e4m3fn).max (dan/quant.py:15-16)
+
+
+def quantize_e4m3(x):
+    """Per-tensor OCP e4m3 as dan/fused.py:85-91 (rowwise=False) with the
+    dan/quant.py:15-16, 28-31 conventions: scale = max(amax|x|, 1e-12) / 448,
+    xq = (x / scale) in float8_e4m3fn, so x ~ xq * scale. Returns (xq, scale)
+    with scale a one-element fp32 tensor on x's device."""
+    xf = x.float()
+    scale = xf.abs().amax().clamp(min=1e-12).reshape(1) / E4M3_MAX
+    return (xf / scale).to(torch.float8_e4m3fn), scale
+
+
+def to_e4m3(w):
+    """The workload with q, k, v and every prefix-cache entry quantized per
+    tensor (each with its own scale). Segments are copied; one shared cache
+    entry stays shared. The scales are in ``meta`` (q_scale, k_scale,
+    v_scale); an e4m3 cache entry is (k, v, k_scale, v_scale)."""
+    (qq, qs), (kq, ks), (vq, vs) = quantize_e4m3(w.q), quantize_e4m3(w.k), quantize_e4m3(w.v)
+    entries, segs = {}, Batch()
+    for s in w.segments:
+        past = None
+        if s.past:
+            past = entries.get(id(s.past))
+            if past is None:
+                pk, pv = s.past[w.layer][:2]
+                (pkq, pks), (pvq, pvs) = quantize_e4m3(pk), quantize_e4m3(pv)
+                past = entries[id(s.past)] = {w.layer: (pkq, pvq, pks, pvs)}
+        segs.append(replace(s, past=past, saved={}, _mask=None))
+    meta = dict(w.meta, q_scale=qs, k_scale=ks, v_scale=vs, source=w.name)
+    return Workload(w.name + "-e4m3", qq, kq, vq, segs, w.layer, meta)
+
+
+def config5(seed=0, device="cpu"):
+    """Config 3's inputs quantized per tensor to OCP e4m3 (q, k, v, and the
+    prefix-cache k and v, each with its own fp32 scale); bf16 output."""
+    return to_e4m3(config3(seed, device))
+
+
 def runner_shapes(seed=0, device="cpu", dtype=torch.bfloat16, head_dim=128):
     """The differential shapes of the reference's kernel test
     (tests/test_runner.py:52-55): h=8, hkv=2, (trunk, [branch lengths], past)
@@ -187,4 +248,4 @@ def runner_shapes(seed=0, device="cpu", dtype=torch.bfloat16, head_dim=128):
                  per_segment_past=[p for _, _, p in shapes])
 
 
-CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4}
+CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4, "c5": config5}

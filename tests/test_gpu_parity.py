@@ -6,6 +6,7 @@ label-softmax readout (rms_norm of the read row, seeded label heads,
 softmax) within 1e-3 in probability."""
 import math
 import sys
+from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -35,7 +36,7 @@ def readout_dp(out, ref, segments, width):
     return max(abs(a - b) for x, y in zip(pa, pb) for a, b in zip(x, y))
 
 
-def check(w, name, atol=ATOL, readout=True):
+def check(w, name, atol=ATOL, readout=True, ref=None, readout_atol=READOUT_ATOL):
     """max-abs against the fp32 oracle; readout against the oracle's output
     rounded to the kernel's output dtype. The output tensor has q's dtype (as
     in the reference), and rounding even an exact fp32 result to bf16 moves
@@ -44,10 +45,12 @@ def check(w, name, atol=ATOL, readout=True):
     unrounded fp32 oracle is reported too."""
     say(f"{name}: N={w.num_tokens} H={w.q.shape[0]} Hkv={w.k.shape[0]} D={w.q.shape[2]} {w.q.dtype} "
         f"segments={len(w.segments)}")
-    out = attend(w.q, w.k, w.v, w.segments, w.layer)
+    out = attend(w.q, w.k, w.v, w.segments, w.layer, **w.attend_kwargs)
     torch.cuda.synchronize()
-    assert out.shape == w.q.shape and out.dtype == w.q.dtype
-    ref = O.attend_dense(w.q, w.k, w.v, w.segments, w.layer)
+    want_dtype = torch.bfloat16 if w.q.dtype == torch.float8_e4m3fn else w.q.dtype
+    assert out.shape == w.q.shape and out.dtype == want_dtype
+    if ref is None:
+        ref = O.attend_dense(w.q, w.k, w.v, w.segments, w.layer)
     got = out.float().cpu()
     rows = torch.cat([torch.arange(s.start, s.end) for s in w.segments])
     err = (got[:, rows] - ref[:, rows]).abs().max().item()
@@ -58,7 +61,7 @@ def check(w, name, atol=ATOL, readout=True):
         dp32 = readout_dp(out.cpu(), ref, w.segments, width)
     say(f"{name}: max-abs {err:.3e}, readout dp {dp:.2e} (vs fp32 oracle output: {dp32:.2e})")
     assert math.isfinite(err) and err <= atol, f"{name}: max-abs {err:.3e} > {atol}"
-    assert dp <= READOUT_ATOL, f"{name}: readout |dp| {dp:.2e} > {READOUT_ATOL}"
+    assert dp <= readout_atol, f"{name}: readout |dp| {dp:.2e} > {readout_atol}"
     return out, ref
 
 
@@ -155,6 +158,68 @@ def test_running_max_raised_by_growing_scores(gpu):
     w = _scored_batch(gpu, [(1000, [40, 24])], lambda t: (np.full(t.shape, 4.0, np.float32),
                                                           0.1 * t.astype(np.float32)))
     check(w, "growing scores")
+
+
+def dequantized(w):
+    """An e4m3 workload with q, k, v and every cache entry dequantized to fp32
+    (x = xq * scale), for the oracle."""
+    m = w.meta
+    entries, segs = {}, Batch()
+    for s in w.segments:
+        past = None
+        if s.past:
+            past = entries.get(id(s.past))
+            if past is None:
+                pk, pv, pks, pvs = s.past[w.layer]
+                past = entries[id(s.past)] = {w.layer: (O.dequantize(pk, pks), O.dequantize(pv, pvs))}
+        segs.append(replace(s, past=past, saved={}, _mask=None))
+    return W.Workload(w.name + "-dq", O.dequantize(w.q, m["q_scale"]), O.dequantize(w.k, m["k_scale"]),
+                      O.dequantize(w.v, m["v_scale"]), segs, w.layer, {})
+
+
+def _fp8_case(w_orig, name, gpu, vs_original=True):
+    """e4m3 kernel output (1) against the oracle on the dequantized inputs --
+    the kernel's own error, held to the bf16 bars (max-abs 2e-2, readout
+    1e-3) -- and (2) against the oracle on the original inputs: max-abs 5e-2
+    (pre-registered) and readout within 1e-2 of the quantization floor. The
+    floor (oracle on dequantized vs oracle on original inputs) is what
+    quantizing q, k, v to e4m3 costs before any kernel runs; on config 5 its
+    readout |dp| (2.6e-2 at seed 0) already exceeds the pre-registered 1e-2,
+    so that bar is applied on top of it."""
+    w8 = W.to_e4m3(w_orig)
+    ref = O.attend_dense(w_orig.q, w_orig.k, w_orig.v, w_orig.segments, w_orig.layer)
+    wd = dequantized(w8)
+    ref_dq = O.attend_dense(wd.q, wd.k, wd.v, wd.segments, wd.layer)
+    rows = torch.cat([torch.arange(s.start, s.end) for s in w_orig.segments])
+    floor = (ref_dq[:, rows] - ref[:, rows]).abs().max().item()
+    dpf = 0.0
+    if any(s.branches for s in w_orig.segments):
+        dpf = readout_dp(ref_dq, ref, w_orig.segments, w_orig.q.shape[0] * w_orig.q.shape[2])
+    say(f"{name}: quantization floor (oracle, dequantized vs original inputs): max-abs {floor:.3e}, readout dp {dpf:.2e}")
+    check(w8, f"{name} vs oracle on dequantized inputs", atol=ATOL, ref=ref_dq)
+    if vs_original:
+        check(w8, f"{name} vs oracle on original inputs", atol=5e-2, ref=ref, readout_atol=dpf + 1e-2)
+
+
+def test_fp8_config5(gpu):
+    """Config 5: config 3 quantized per tensor to OCP e4m3."""
+    _fp8_case(W.config3(0, device=gpu), "c5 seed 0 (e4m3)", gpu)
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_fp8_reference_shapes(gpu, head_dim):
+    """The differential shapes with per-segment e4m3 cache entries (12 and 20
+    keys: tiles holding both cache and new keys take the k-scale fix-up).
+    Held to the oracle on the dequantized inputs only: with N(0,1) inputs and
+    rows of a few keys the quantization floor itself is ~0.18 max-abs."""
+    _fp8_case(W.runner_shapes(0, device=gpu, dtype=torch.bfloat16, head_dim=head_dim),
+              f"e4m3 runner shapes D={head_dim}", gpu, vs_original=False)
+
+
+def test_fp8_needs_scales(gpu):
+    w8 = W.to_e4m3(W.config1(0, device=gpu))
+    with pytest.raises(ValueError, match="scale"):
+        attend(w8.q, w8.k, w8.v, w8.segments, 0)
 
 
 def test_fp32_config1_layout(gpu):

@@ -245,3 +245,31 @@ def test_useful_pairs_counts_the_mask():
     w = W.runner_shapes(0, dtype=torch.float32)
     total = sum(O.visible(s.trunk, list(s.branch_ids), s.past_len).sum() for s in w.segments)
     assert O.useful_pairs(w.segments) == total
+
+
+def test_package_useful_pairs_matches_oracle_closed_form():
+    """The package's per-query count (used by bench.py) against the oracle's
+    closed form, which test_useful_pairs_counts_the_mask pins to the mask."""
+    from dan_amd import workloads as W
+    for cfg in ("c1", "c2", "c3", "c4"):
+        w = W.CONFIGS[cfg](0)
+        assert W.useful_pairs(w.segments) == O.useful_pairs(w.segments), cfg
+    w = W.runner_shapes(0)
+    assert W.useful_pairs(w.segments) == O.useful_pairs(w.segments)
+
+
+def test_package_e4m3_quantization_matches_oracle():
+    """dan_amd.workloads.quantize_e4m3 (the config-5 input generator) against
+    the oracle's restatement of dan/fused.py:85-91: same bytes, same scale;
+    and a shared prefix-cache entry stays one shared e4m3 entry."""
+    from dan_amd import workloads as W
+    x = torch.from_numpy(np.random.default_rng(3).standard_normal((4, 100, 64)).astype(np.float32) * 3)
+    xq, s = W.quantize_e4m3(x)
+    oq, os_ = O.fp8_quantize(x)
+    assert torch.equal(xq.view(torch.uint8), oq.view(torch.uint8))
+    assert torch.equal(s.reshape(()), os_.reshape(()))
+    w = W.to_e4m3(W.config3(0))
+    entries = {id(seg.past) for seg in w.segments if seg.past}
+    assert len(entries) == 1
+    pk, pv, pks, pvs = w.segments[0].past[0]
+    assert pk.dtype == pv.dtype == torch.float8_e4m3fn and pks.numel() == pvs.numel() == 1
