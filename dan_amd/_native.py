@@ -18,13 +18,14 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 KEY_TILE = 64
 
 # DanStatus
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_VERSION = range(5)
 # DanDtype
 DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_E4M3 = range(4)
+PHASES_ALL, PHASE_PACK, PHASE_ATTEND = 0, 1, 2
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -62,7 +63,7 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("key_lo", _vp),
                 ("tile_q", _i32), ("vt_cols", _i32),
                 ("col_seg", _vp),
-                ("workspace", _vp), ("workspace_bytes", _i64)]
+                ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32)]
 
 
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_workspace_size", "dan_tree_attn_last_error",

@@ -255,7 +255,10 @@ def _workspace(plan, nbytes, device):
     return ws
 
 
-def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None):
+def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL):
+    """The kernel call behind ``attend`` (no save side effect). ``phases``
+    selects the launches (the C ABI's ``phases``): bench.py times the
+    attention launch alone with PHASE_ATTEND after a full call."""
     if not q.is_cuda:
         raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
                            f"{q.device} (the masked CPU path is the test oracle, not a backend)")
@@ -302,5 +305,6 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None):
         a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
         if q.dtype == E4M3:
             a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
+        a.phases = phases
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

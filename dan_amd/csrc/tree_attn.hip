@@ -852,6 +852,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   if (f8 && (!a->q_scale || !a->k_scale || !a->v_scale))
     return fail(DAN_ERR_INVALID_ARGUMENT, "e4m3 inputs need q_scale, k_scale and v_scale");
   if (!(a->scale > 0.f) || !isfinite(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
+  if (a->phases < DAN_TREE_ATTN_PHASES_ALL || a->phases > DAN_TREE_ATTN_PHASE_ATTEND)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "phases %d: 0 (all), 1 (pack) or 2 (attend)", a->phases);
   const int64_t need = dan_tree_attn_workspace_size(Hkv, D, a->vt_cols);
   if (a->vt_cols <= 0 || need <= 0) return fail(DAN_ERR_INVALID_ARGUMENT, "vt_cols %d must be a positive multiple of %d", a->vt_cols, kKeyTile);
   if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255))
@@ -884,12 +886,15 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool d128 = D == 128;
-  hipError_t err;
+  hipError_t err = hipSuccess;
+  if (a->phases != DAN_TREE_ATTN_PHASE_ATTEND) {
   if (bf16) err = d128 ? launch_pack<__bf16, 128>(pp, (int)pack_grid, s) : launch_pack<__bf16, 64>(pp, (int)pack_grid, s);
   else if (f16) err = d128 ? launch_pack<_Float16, 128>(pp, (int)pack_grid, s) : launch_pack<_Float16, 64>(pp, (int)pack_grid, s);
   else if (f8) err = d128 ? launch_pack<E4M3, 128>(pp, (int)pack_grid, s) : launch_pack<E4M3, 64>(pp, (int)pack_grid, s);
   else err = d128 ? launch_pack<float, 128>(pp, (int)pack_grid, s) : launch_pack<float, 64>(pp, (int)pack_grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "V^T pack launch failed: %s", hipGetErrorString(err));
+  }
+  if (a->phases == DAN_TREE_ATTN_PHASE_PACK) return DAN_OK;
 
   if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, (int)grid, s) : launch_attn<__bf16, __bf16, 64>(kp, (int)grid, s);
   else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, (int)grid, s) : launch_attn<_Float16, _Float16, 64>(kp, (int)grid, s);

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 2
+#define DAN_TREE_ATTN_ABI_VERSION 3
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -110,9 +110,9 @@ typedef struct {
 
 typedef struct {
   int32_t abi_version; /* DAN_TREE_ATTN_ABI_VERSION */
-  int32_t in_dtype;    /* DanDtype of q, k and the pasts' k: bf16 or f16 */
-  int32_t out_dtype;   /* DanDtype of out: bf16, f16 or f32 */
-  int32_t v_dtype;     /* DanDtype of v and the pasts' v: bf16, f16 or f32 */
+  int32_t in_dtype;    /* DanDtype of q, k and the pasts' k: bf16, f16 or e4m3 */
+  int32_t out_dtype;   /* DanDtype of out: bf16, f16 or f32 (bf16 for e4m3) */
+  int32_t v_dtype;     /* DanDtype of v and the pasts' v: bf16, f16, f32 or e4m3 */
   int32_t num_heads;   /* H */
   int32_t num_kv_heads;/* Hkv; query head h reads kv head h / (H / Hkv) */
   int32_t head_dim;    /* D: 64 or 128 */
@@ -146,7 +146,17 @@ typedef struct {
    * same stream. */
   void *workspace;
   int64_t workspace_bytes;
+  /* Which of the two launches to make: DAN_TREE_ATTN_PHASES_ALL (0: the V^T
+   * copy, then attention), DAN_TREE_ATTN_PHASE_PACK (the copy only) or
+   * DAN_TREE_ATTN_PHASE_ATTEND (attention only, reading a workspace a
+   * previous call filled for the same v and pasts) -- for callers that
+   * overlap the copy with other work, and for timing each launch. */
+  int32_t phases;
 } DanTreeAttnArgs;
+
+#define DAN_TREE_ATTN_PHASES_ALL 0
+#define DAN_TREE_ATTN_PHASE_PACK 1
+#define DAN_TREE_ATTN_PHASE_ATTEND 2
 
 /* Fused tree-masked attention forward: out = softmax(scale * q k^T + mask) v
  * over every (query, visible key) pair of every segment, in one launch.

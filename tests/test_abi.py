@@ -55,6 +55,7 @@ def test_ctypes_layout_matches_header(tmp_path):
             lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
     lines.append(f'printf("ABI %d\\n", DAN_TREE_ATTN_ABI_VERSION);')
     lines.append(f'printf("KEY_TILE %d\\n", DAN_TREE_ATTN_KEY_TILE);')
+    lines.append('printf("PHASES %d,%d,%d\\n", DAN_TREE_ATTN_PHASES_ALL, DAN_TREE_ATTN_PHASE_PACK, DAN_TREE_ATTN_PHASE_ATTEND);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -69,6 +70,7 @@ def test_ctypes_layout_matches_header(tmp_path):
             assert int(got[f"{cname}.{fname}"]) == getattr(cls, fname).offset, f"{cname}.{fname}"
     assert int(got["ABI"]) == _native.ABI_VERSION
     assert int(got["KEY_TILE"]) == _native.KEY_TILE
+    assert got["PHASES"] == f"{_native.PHASES_ALL},{_native.PHASE_PACK},{_native.PHASE_ATTEND}"
 
 
 def test_abi_version_and_tile_q(lib):
@@ -101,6 +103,8 @@ def _args(**kw):
     (dict(tile_q=32), _native.ERR_INVALID_ARGUMENT, "tile_q"),
     (dict(num_work=3), _native.ERR_INVALID_ARGUMENT, "NULL"),
     (dict(num_work=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+    (dict(in_dtype=_native.DTYPE_E4M3, v_dtype=_native.DTYPE_E4M3, out_dtype=_native.DTYPE_F16),
+     _native.ERR_UNSUPPORTED, "dtype"),
 ])
 def test_argument_errors(lib, kw, status, needle):
     rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**kw)), None)
@@ -139,3 +143,9 @@ def test_bad_scale_dtype_and_workspace(lib):
     assert lib.dan_tree_attn_fwd(ctypes.byref(_args(**odd)), None) == _native.ERR_INVALID_ARGUMENT
     bad = _args(**dict(full, v_dtype=_native.DTYPE_E4M3))
     assert lib.dan_tree_attn_fwd(ctypes.byref(bad), None) == _native.ERR_UNSUPPORTED
+    f8 = _args(**dict(full, in_dtype=_native.DTYPE_E4M3, v_dtype=_native.DTYPE_E4M3))  # no scales
+    assert lib.dan_tree_attn_fwd(ctypes.byref(f8), None) == _native.ERR_INVALID_ARGUMENT
+    assert "scale" in _native.last_error(lib)
+    ph = _args(**dict(full, phases=3))
+    assert lib.dan_tree_attn_fwd(ctypes.byref(ph), None) == _native.ERR_INVALID_ARGUMENT
+    assert "phases" in _native.last_error(lib)
