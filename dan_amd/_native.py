@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 KEY_TILE = 64
 
 # DanStatus
@@ -63,11 +63,12 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("key_lo", _vp),
                 ("tile_q", _i32), ("vt_cols", _i32),
                 ("col_seg", _vp),
-                ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32)]
+                ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32),
+                ("sched", _vp), ("sched_off", _vp), ("num_slots", _i32)]
 
 
-EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_workspace_size", "dan_tree_attn_last_error",
-           "dan_tree_attn_abi_version")
+EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
+           "dan_tree_attn_last_error", "dan_tree_attn_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -89,6 +90,8 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_fwd.restype = ctypes.c_int
         lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
         lib.dan_tree_attn_tile_q.restype = ctypes.c_int
+        lib.dan_tree_attn_head_groups.argtypes = [_i32, _i32]
+        lib.dan_tree_attn_head_groups.restype = ctypes.c_int
         lib.dan_tree_attn_workspace_size.argtypes = [_i32, _i32, _i32]
         lib.dan_tree_attn_workspace_size.restype = _i64
         lib.dan_tree_attn_last_error.argtypes = []
@@ -111,6 +114,11 @@ def last_error(lib):
 def tile_q(num_heads, num_kv_heads, lib=None):
     """Queries per work item the kernel expects (0: unsupported head layout)."""
     return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads)
+
+
+def head_groups(num_heads, num_kv_heads, lib=None):
+    """Head groups of the persistent schedule (0: unsupported head layout)."""
+    return (lib or load()).dan_tree_attn_head_groups(num_heads, num_kv_heads)
 
 
 def workspace_size(num_kv_heads, head_dim, vt_cols, lib=None):

@@ -22,6 +22,7 @@ replaces the reference's three varlen flash calls plus log-sum-exp merge
 There is no CPU or fallback path: CPU tensors, a missing library or an
 unsupported shape raise.
 """
+import functools
 import math
 from dataclasses import dataclass, field
 
@@ -255,6 +256,12 @@ def _workspace(plan, nbytes, device):
     return ws
 
 
+@functools.lru_cache(maxsize=None)
+def _num_cus(device):
+    """Compute units of the device (the persistent grid's size)."""
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
 def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL):
     """The kernel call behind ``attend`` (no save side effect). ``phases``
     selects the launches (the C ABI's ``phases``): bench.py times the
@@ -306,5 +313,8 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
         if q.dtype == E4M3:
             a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
         a.phases = phases
+        groups = _native.head_groups(h, hkv, lib)
+        sched, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
+        a.sched, a.sched_off, a.num_slots = sched.data_ptr(), sched_off.data_ptr(), slots
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

@@ -14,14 +14,17 @@
 //   tree_attn_kernel   the attention itself.
 //
 // Work decomposition of tree_attn_kernel
-//   - A work group (8 waves, 2 per SIMD) owns one work item (a tile of query
-//     tokens of one segment) for one kv head. Wave w takes query head
-//     (w % hpw) of the kv group and the (w / hpw)-th run of 32 tokens, so the
-//     K / V^T tiles staged in LDS serve every query head that shares them
-//     (GQA head packing).
-//   - blockIdx.x = item * (Hkv * chunks) + kv head + Hkv * chunk: consecutive
-//     blocks land on different XCDs, so with Hkv = 8 each XCD's L2 holds one
-//     kv head's keys and values.
+//   - A unit is one work item (a tile of query tokens of one segment) for one
+//     head group (kv head + Hkv * chunk). A work group (8 waves, 2 per SIMD)
+//     runs units one after another. Wave w takes query head (w % hpw) of the
+//     kv group and the (w / hpw)-th run of 32 tokens, so the K / V^T tiles
+//     staged in LDS serve every query head that shares them (GQA head
+//     packing).
+//   - The grid is persistent: about one work group per CU, each walking a
+//     host-planned list of units with balanced key-tile counts (one launch
+//     wave, no tail of short work groups). Work group b runs on XCD b % 8
+//     and gets only units of head group b % groups, so with Hkv = 8 each
+//     XCD's L2 holds one kv head's keys and values.
 //
 // Per wave and key tile of 64 keys:
 //   S^T[key, query] = K Q^T      v_mfma_f32_32x32x16 (bf16 or fp16): A = K rows
@@ -111,7 +114,14 @@ struct KParams {
   // e4m3 only: per-tensor scales of q and k (device fp32 scalars); S is
   // scaled by q_scale * k_scale (a prefix-cache entry has its own k scale).
   const float *q_scale, *k_scale;
+  // Persistent schedule: work group b runs units sched[sched_off[b]] ..
+  // sched[sched_off[b + 1] - 1]; unit u = work item u / groups, head group
+  // u % groups.
+  const int32_t *sched, *sched_off;
+  int32_t num_units;
 };
+
+typedef const __attribute__((address_space(4))) KParams *KArgPtr;
 
 struct PackParams {
   const void *v;
@@ -430,7 +440,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
 // bf16's 8 (or e4m3's 4), and the V^T copy is fp16.
 template <typename TQK, typename TOut, int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
-void tree_attn_kernel(const KParams p) {
+void tree_attn_kernel(const KParams args) {
   using L = Lds<D, (int)sizeof(TQK)>;
   constexpr bool kF8 = std::is_same<TQK, E4M3>::value;
   constexpr int KS = QK<TQK>::step;                   // k-step of Q K^T
@@ -446,331 +456,352 @@ void tree_attn_kernel(const KParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, lq = lane & 31;
 
-  const int groups = p.num_kv_heads * p.chunks;
-  const DanWorkItem w = load_entry(p.work + blockIdx.x / groups);
-  const int g = blockIdx.x % groups;
-  const int kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
-  const DanSegmentDesc sg = load_entry(p.segs + w.seg);
-  const int P = sg.past_len, PT = P + sg.trunk, PN = P + sg.n;
-  const int H = p.num_kv_heads * p.rep;
+  // sched holds num_units entries: clamping the range keeps a malformed
+  // offset table from reading past it.
+  const int u_begin = max(*gbl(args.sched_off + blockIdx.x), 0);
+  const int u_end = min(*gbl(args.sched_off + blockIdx.x + 1), args.num_units);
+  // `args` is the first (and only) explicit kernel argument, at the start of
+  // the kernarg segment. Each unit reads its fields through an opaque copy
+  // of that address, so they are reloaded per unit (scalar loads) instead of
+  // being hoisted out of the unit loop and held in SGPRs across the key
+  // loop, where they would spill.
+  const KArgPtr kseg = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  for (int u = u_begin; u < u_end; ++u) {
+    KArgPtr kp_u = kseg;
+    asm volatile("" : "+s"(kp_u));
+    const KParams &p = *(const KParams *)kp_u;
+    const int groups = p.num_kv_heads * p.chunks;
+    const int unit = __builtin_amdgcn_readfirstlane(*gbl(p.sched + u));
+    if (unit < 0 || unit >= p.num_units) continue;  // a malformed schedule entry: skip it
+    // Every wave is done with the previous unit's stage buffers before this
+    // unit's first tiles are loaded into them.
+    barrier_lds();
+    const DanWorkItem w = load_entry(p.work + unit / groups);
+    const int g = unit % groups;
+    const int kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
+    const DanSegmentDesc sg = load_entry(p.segs + w.seg);
+    const int P = sg.past_len, PT = P + sg.trunk, PN = P + sg.n;
+    const int H = p.num_kv_heads * p.rep;
 
-  const int hig = chunk * p.hpw + (wave % p.hpw);
-  const int head = kvh * p.rep + hig;
-  const int qw0 = w.t0 + (wave / p.hpw) * kWaveQ;  // wave's first query (segment-local)
-  const int qend = w.t0 + w.tq;
-  const bool wave_work = hig < p.rep && qw0 < qend;
+    const int hig = chunk * p.hpw + (wave % p.hpw);
+    const int head = kvh * p.rep + hig;
+    const int qw0 = w.t0 + (wave / p.hpw) * kWaveQ;  // wave's first query (segment-local)
+    const int qend = w.t0 + w.tq;
+    const bool wave_work = hig < p.rep && qw0 < qend;
 
-  const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
-  const TQK *pkp = nullptr;
-  int64_t pk_st = 0;
-  // Softmax exponent factor c of S: scale * log2(e), times q_scale * k_scale
-  // for e4m3 (the prefix-cache entry's k has its own scale, c_past).
-  float c_new = p.c, c_past = p.c;
-  if (kF8) c_new = c_past = p.c * *gbl(p.q_scale) * *gbl(p.k_scale);
-  if (P > 0) {
-    const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
-    pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
-    pk_st = pd.k_stride_tok;
-    if (kF8) c_past = p.c * *gbl(p.q_scale) * *gbl(pd.k_scale);
-  }
-  const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
+    const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
+    const TQK *pkp = nullptr;
+    int64_t pk_st = 0;
+    // Softmax exponent factor c of S: scale * log2(e), times q_scale * k_scale
+    // for e4m3 (the prefix-cache entry's k has its own scale, c_past).
+    float c_new = p.c, c_past = p.c;
+    if (kF8) c_new = c_past = p.c * *gbl(p.q_scale) * *gbl(p.k_scale);
+    if (P > 0) {
+      const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
+      pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
+      pk_st = pd.k_stride_tok;
+      if (kF8) c_past = p.c * *gbl(p.q_scale) * *gbl(pd.k_scale);
+    }
+    const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
 
-  // Per-lane query state: lane owns query column lq of its wave. Padding
-  // columns (past the tile, or an idle wave) read a clamped valid row and see
-  // every key, so they stay finite; they are never stored.
-  const int ql = qw0 + lq;
-  const bool qvalid = wave_work && ql < qend;
-  const int qrow = sg.start + min(ql, qend - 1);
-  const int qk = qvalid ? P + ql : 0x3fffffff;
-  const int qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
-  Frag<TQK> qf[NK];
-  {
-    const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
+    // Per-lane query state: lane owns query column lq of its wave. Padding
+    // columns (past the tile, or an idle wave) read a clamped valid row and see
+    // every key, so they stay finite; they are never stored.
+    const int ql = qw0 + lq;
+    const bool qvalid = wave_work && ql < qend;
+    const int qrow = sg.start + min(ql, qend - 1);
+    const int qk = qvalid ? P + ql : 0x3fffffff;
+    const int qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
+    Frag<TQK> qf[NK];
+    {
+      const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
-  }
-  // Raw score of the query against its own key (key coordinate P + query,
-  // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
-  auto self_score = [&](const Frag<TQK>(&q)[NK], int qr) __attribute__((always_inline)) {
-    const TQK *krow = kp + (int64_t)qr * p.k_st + KS / 2 * hl;
-    float acc = 0.f;
+      for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
+    }
+    // Raw score of the query against its own key (key coordinate P + query,
+    // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
+    auto self_score = [&](const Frag<TQK>(&q)[NK], int qr) __attribute__((always_inline)) {
+      const TQK *krow = kp + (int64_t)qr * p.k_st + KS / 2 * hl;
+      float acc = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) acc = dot_frag<TQK>(q[kk], load_frag<TQK>(krow + KS * kk), acc);
-    const LanePair lp = lane_pair(acc);
-    return lp.self + lp.other;
-  };
-
-  // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
-  // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
-  // VF V^T blocks, and one last slot that takes a leftover K or V^T block or
-  // goes to the sink. Per-lane element offsets from the tile's first row are
-  // loop-invariant; K keeps one per source layout (new tokens / past).
-  constexpr int KF = L::kInsts / kWaves, VF = L::vInsts / kWaves;
-  constexpr int KREM = L::kInsts - KF * kWaves, VREM = L::vInsts - VF * kWaves;
-  static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
-  const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
-  const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
-  auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
-    const int pos = blk * 64 + lane;
-    return (uint32_t)(k_row(pos / KC) * st + CE * min(pos % KC, KC - 2));
-  };
-  auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
-    const int pos = blk * 64 + lane;
-    return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
-  };
-  uint32_t kon[KF > 0 ? KF : 1], kop[KF > 0 ? KF : 1], von[VF > 0 ? VF : 1];  // (KF is 0 for e4m3, D = 64)
-#pragma unroll
-  for (int s = 0; s < KF; ++s) {
-    kon[s] = k_offset(wave + kWaves * s, p.k_st);
-    kop[s] = k_offset(wave + kWaves * s, pk_st);
-  }
-#pragma unroll
-  for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
-  // last slot: K offsets (new, past) or the V^T / sink offset
-  const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
-  const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
-  const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
-
-  // Issue the direct loads of key tile j into stage buffer b.
-  auto issue = [&](int j, int b) __attribute__((always_inline)) {
-    const int kb = j * kKeyTile;
-    uint8_t *base = smem + b * L::buf;
-    const _Float16 *vtt = vtp + kb;
-    auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
-      const int pos = blk * 64 + lane;
-      const int col = CE * min(pos % KC, KC - 2);
-      const int key = min(kb + k_row(pos / KC), PN - 1);
-      return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
+      for (int kk = 0; kk < NK; ++kk) acc = dot_frag<TQK>(q[kk], load_frag<TQK>(krow + KS * kk), acc);
+      const LanePair lp = lane_pair(acc);
+      return lp.self + lp.other;
     };
-    // (Separate loops per source layout: a select between two offset arrays
-    // would make the compiler keep them in scratch memory.)
-    if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
-      const TQK *tb = pkp + (int64_t)kb * pk_st;
+
+    // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
+    // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
+    // VF V^T blocks, and one last slot that takes a leftover K or V^T block or
+    // goes to the sink. Per-lane element offsets from the tile's first row are
+    // loop-invariant; K keeps one per source layout (new tokens / past).
+    constexpr int KF = L::kInsts / kWaves, VF = L::vInsts / kWaves;
+    constexpr int KREM = L::kInsts - KF * kWaves, VREM = L::vInsts - VF * kWaves;
+    static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
+    const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
+    const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
+    auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
+      const int pos = blk * 64 + lane;
+      return (uint32_t)(k_row(pos / KC) * st + CE * min(pos % KC, KC - 2));
+    };
+    auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
+      const int pos = blk * 64 + lane;
+      return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
+    };
+    uint32_t kon[KF > 0 ? KF : 1], kop[KF > 0 ? KF : 1], von[VF > 0 ? VF : 1];  // (KF is 0 for e4m3, D = 64)
 #pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
-    } else if (kb >= P && kb + kKeyTile <= PN) {
-      const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
-#pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
-    } else {
-#pragma unroll
-      for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
-      if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
+    for (int s = 0; s < KF; ++s) {
+      kon[s] = k_offset(wave + kWaves * s, p.k_st);
+      kop[s] = k_offset(wave + kWaves * s, pk_st);
     }
 #pragma unroll
-    for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
-    if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
-    if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
-  };
+    for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
+    // last slot: K offsets (new, past) or the V^T / sink offset
+    const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
+    const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
+    const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
 
-  f32x16 o[ND];
+    // Issue the direct loads of key tile j into stage buffer b.
+    auto issue = [&](int j, int b) __attribute__((always_inline)) {
+      const int kb = j * kKeyTile;
+      uint8_t *base = smem + b * L::buf;
+      const _Float16 *vtt = vtp + kb;
+      auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
+        const int pos = blk * 64 + lane;
+        const int col = CE * min(pos % KC, KC - 2);
+        const int key = min(kb + k_row(pos / KC), PN - 1);
+        return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
+      };
+      // (Separate loops per source layout: a select between two offset arrays
+      // would make the compiler keep them in scratch memory.)
+      if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
+        const TQK *tb = pkp + (int64_t)kb * pk_st;
 #pragma unroll
-  for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-  // Exponent offset -m of the running max m, which starts at the query's
-  // score against its own key (always visible to it).
-  float mneg = -self_score(qf, qrow) * c_new, lsum = 0.f;
-  u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
+        for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
+      } else if (kb >= P && kb + kKeyTile <= PN) {
+        const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
+#pragma unroll
+        for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
+      } else {
+#pragma unroll
+        for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
+      }
+#pragma unroll
+      for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
+      if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
+      if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
+    };
 
-  // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
-  auto qk_phase = [&](int b, f32x16(&s)[2]) {
-    const uint8_t *kbuf = smem + b * L::buf;
-    s[0] = f32x16{};
-    s[1] = f32x16{};
+    f32x16 o[ND];
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
+    for (int db = 0; db < ND; ++db) o[db] = f32x16{};
+    // Exponent offset -m of the running max m, which starts at the query's
+    // score against its own key (always visible to it).
+    float mneg = -self_score(qf, qrow) * c_new, lsum = 0.f;
+    u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
+
+    // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
+    auto qk_phase = [&](int b, f32x16(&s)[2]) {
+      const uint8_t *kbuf = smem + b * L::buf;
+      s[0] = f32x16{};
+      s[1] = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          Frag<TQK> a;
+#pragma unroll
+          for (int i = 0; i < QK<TQK>::chunks; ++i)
+            a.c[i] = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow +
+                                                      ((2 * kk + hl) * QK<TQK>::chunks + i) * 16);
+          s[mb] = mfma_qk<TQK>(a, qf[kk], s[mb]);
+        }
+      }
+    };
+    // Tree mask on boundary tiles. Key index of register r relative to the tile
+    // start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
+    // sibling-branch gap are per-lane bounds on it; the gap test runs only on
+    // tiles meeting [PT, lo_max).
+    auto mask_phase = [&](int j, f32x16(&s)[2]) {
+      if (j < w.jfull) return;
+      const int kb = j * kKeyTile;
+      const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
+      if (kb + kKeyTile > PT && kb < w.lo_max) {
+        const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+            const bool vis = rel <= lim && (rel < g0 || rel >= g1);
+            s[mb][r] = vis ? s[mb][r] : -INFINITY;
+          }
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+            s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
+          }
+      }
+    };
+    // Exponent factor of tile j's scores, and (e4m3) the fix-up of a tile that
+    // holds both prefix-cache and new keys: the prefix keys' scores are brought
+    // to the new keys' k scale, and the tile then uses c_new.
+    auto tile_c = [&](int j) __attribute__((always_inline)) { return j * kKeyTile + kKeyTile <= P ? c_past : c_new; };
+    auto fix_straddle = [&](int j, f32x16(&s)[2]) __attribute__((always_inline)) {
+      const int kb = j * kKeyTile;
+      if (!kF8 || !(kb < P && kb + kKeyTile > P)) return;
+      const float ratio = c_past / c_new;
+      const int lim = P - kb - 8 * hl;  // prefix key: rel < lim
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
+          s[mb][r] = rel < lim ? s[mb][r] * ratio : s[mb][r];
+        }
+    };
+    // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
+    // partial row sum of the fp16-rounded values that P V uses (exact products,
+    // fp32 accumulation), so rounding P mostly cancels in O / l. The running
+    // max m starts at tile 0's max and is not recomputed per tile: a partial
+    // row sum above kSumLimit (or inf) means some p left fp16's range or m is
+    // stale by more than log2(kSumLimit / 32); only then is m raised to the
+    // tile's max (O and l rescaled) and the tile's P redone. A lane holds half
+    // of its query's keys and the other half sits in lane ^ 32; both keep the
+    // same m.
+    auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
+      float m8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
+#pragma unroll
+      for (int w2 = 4; w2 >= 1; w2 >>= 1)
+#pragma unroll
+        for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
+      const LanePair mp = lane_pair(m8[0]);
+      return fmaxf(mp.self, mp.other);
+    };
+    auto exp_phase = [&](const f32x16(&s)[2], float c) __attribute__((always_inline)) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        Frag<TQK> a;
+        f32x8 x0, x1;
 #pragma unroll
-        for (int i = 0; i < QK<TQK>::chunks; ++i)
-          a.c[i] = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow +
-                                                    ((2 * kk + hl) * QK<TQK>::chunks + i) * 16);
-        s[mb] = mfma_qk<TQK>(a, qf[kk], s[mb]);
-      }
-    }
-  };
-  // Tree mask on boundary tiles. Key index of register r relative to the tile
-  // start: 32*mb + 16*(r/8) + 8*hl + r%8. The causal limit and the
-  // sibling-branch gap are per-lane bounds on it; the gap test runs only on
-  // tiles meeting [PT, lo_max).
-  auto mask_phase = [&](int j, f32x16(&s)[2]) {
-    if (j < w.jfull) return;
-    const int kb = j * kKeyTile;
-    const int lim = qk - kb - 8 * hl;  // visible: rel <= lim
-    if (kb + kKeyTile > PT && kb < w.lo_max) {
-      const int g0 = PT - kb - 8 * hl, g1 = qlo - kb - 8 * hl;  // hidden: g0 <= rel < g1
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-          const bool vis = rel <= lim && (rel < g0 || rel >= g1);
-          s[mb][r] = vis ? s[mb][r] : -INFINITY;
+        for (int r = 0; r < 8; ++r) {
+          x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], c, mneg));
+          x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], c, mneg));
         }
-    } else {
+        pf[2 * mb] = pack8<_Float16>(x0);
+        pf[2 * mb + 1] = pack8<_Float16>(x1);
+      }
+      float acc[4];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int kj = 0; kj < 4; ++kj) {  // four short chains instead of one long one
+        const f16x8 h = __builtin_bit_cast(f16x8, pf[kj]);
+        acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), kOnes2, 0.f, false);
+        acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), kOnes2, acc[kj], false);
+        acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc[kj], false);
+        acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc[kj], false);
+      }
+      return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    };
+    // Accept the tile's P (partial sum ts), raising m to the tile's max (and
+    // redoing P) first if it overflowed.
+    auto finish_tile = [&](const f32x16(&s)[2], float ts, float c) __attribute__((always_inline)) {
+      if (__any(!(ts <= kSumLimit))) {
+        const float mold = -mneg;
+        const float mnew = fmaxf(mold, s_max(s) * c);
+        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+        mneg = -mnew;
+        lsum *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-          s[mb][r] = rel <= lim ? s[mb][r] : -INFINITY;
+        for (int db = 0; db < ND; ++db) o[db] *= alpha;
+        ts = exp_phase(s, c);
+      }
+      lsum += ts;
+    };
+    // O^T += V^T P^T over the 64 keys of stage buffer b.
+    auto pv_phase = [&](int b) __attribute__((always_inline)) {
+      const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
+#pragma unroll
+      for (int kj = 0; kj < 4; ++kj) {
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
+          o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
+        }
+      }
+    };
+
+    const int ntile = w.ja1 + (w.jb1 - w.jb0);
+    auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
+
+    // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      if (t < ntile) issue(tile_of(t), t);
+    if (ntile >= 3) wait_vmem<2 * SLOTS>();
+    else if (ntile == 2) wait_vmem<SLOTS>();
+    else wait_vmem<0>();
+    barrier_lds();
+    f32x16 sa[2], sb[2];
+    if (ntile > 0) {
+      qk_phase(0, sa);
+      mask_phase(tile_of(0), sa);
+      fix_straddle(tile_of(0), sa);
+    }
+
+    // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
+    // core, then O += V P of tile it while the VALU masks S(it+1).
+    // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
+    // barrier of step it), its buffer's previous tile it-1 is finished by every
+    // wave.
+    int it = 0;
+    auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
+      const bool has_next = it + 1 < ntile;
+      if (has_next) {
+        if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+        else wait_vmem<0>();
+        barrier_lds();
+        if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+      }
+      // S of the next tile is computed unconditionally (on the last tile it
+      // reads a stale but complete buffer and is discarded) so that it shares a
+      // basic block with the softmax VALU work and the two interleave.
+      const float c = tile_c(tile_of(it));
+      const float ts = exp_phase(cur, c);
+      qk_phase((it + 1) & 3, nxt);
+      finish_tile(cur, ts, c);
+      pv_phase(it & 3);
+      if (has_next) {
+        mask_phase(tile_of(it + 1), nxt);
+        fix_straddle(tile_of(it + 1), nxt);
+      }
+      ++it;
+    };
+    while (it < ntile) {
+      step(sa, sb);
+      if (it < ntile) step(sb, sa);
+    }
+
+    // Epilogue: O = O^T / l, written token-major [N, H, D].
+    const float l = lsum + __shfl_xor(lsum, 32);
+    const float linv = l > 0.f ? 1.0f / l : 0.f;
+    if (qvalid) {
+      TOut *row = static_cast<TOut *>(p.o) + (int64_t)(sg.start + ql) * p.o_st + (int64_t)head * p.o_sh + 4 * hl;
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 x = {o[db][4 * r4] * linv, o[db][4 * r4 + 1] * linv, o[db][4 * r4 + 2] * linv,
+                           o[db][4 * r4 + 3] * linv};
+          store4<TOut>(row + 32 * db + 8 * r4, x);
         }
     }
-  };
-  // Exponent factor of tile j's scores, and (e4m3) the fix-up of a tile that
-  // holds both prefix-cache and new keys: the prefix keys' scores are brought
-  // to the new keys' k scale, and the tile then uses c_new.
-  auto tile_c = [&](int j) __attribute__((always_inline)) { return j * kKeyTile + kKeyTile <= P ? c_past : c_new; };
-  auto fix_straddle = [&](int j, f32x16(&s)[2]) __attribute__((always_inline)) {
-    const int kb = j * kKeyTile;
-    if (!kF8 || !(kb < P && kb + kKeyTile > P)) return;
-    const float ratio = c_past / c_new;
-    const int lim = P - kb - 8 * hl;  // prefix key: rel < lim
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rel = 32 * mb + 16 * (r >> 3) + (r & 7);
-        s[mb][r] = rel < lim ? s[mb][r] * ratio : s[mb][r];
-      }
-  };
-  // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
-  // partial row sum of the fp16-rounded values that P V uses (exact products,
-  // fp32 accumulation), so rounding P mostly cancels in O / l. The running
-  // max m starts at tile 0's max and is not recomputed per tile: a partial
-  // row sum above kSumLimit (or inf) means some p left fp16's range or m is
-  // stale by more than log2(kSumLimit / 32); only then is m raised to the
-  // tile's max (O and l rescaled) and the tile's P redone. A lane holds half
-  // of its query's keys and the other half sits in lane ^ 32; both keep the
-  // same m.
-  auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
-    float m8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
-#pragma unroll
-    for (int w2 = 4; w2 >= 1; w2 >>= 1)
-#pragma unroll
-      for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
-    const LanePair mp = lane_pair(m8[0]);
-    return fmaxf(mp.self, mp.other);
-  };
-  auto exp_phase = [&](const f32x16(&s)[2], float c) __attribute__((always_inline)) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      f32x8 x0, x1;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        x0[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r], c, mneg));
-        x1[r] = __builtin_amdgcn_exp2f(fmaf(s[mb][r + 8], c, mneg));
-      }
-      pf[2 * mb] = pack8<_Float16>(x0);
-      pf[2 * mb + 1] = pack8<_Float16>(x1);
-    }
-    float acc[4];
-#pragma unroll
-    for (int kj = 0; kj < 4; ++kj) {  // four short chains instead of one long one
-      const f16x8 h = __builtin_bit_cast(f16x8, pf[kj]);
-      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), kOnes2, 0.f, false);
-      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), kOnes2, acc[kj], false);
-      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc[kj], false);
-      acc[kj] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc[kj], false);
-    }
-    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  };
-  // Accept the tile's P (partial sum ts), raising m to the tile's max (and
-  // redoing P) first if it overflowed.
-  auto finish_tile = [&](const f32x16(&s)[2], float ts, float c) __attribute__((always_inline)) {
-    if (__any(!(ts <= kSumLimit))) {
-      const float mold = -mneg;
-      const float mnew = fmaxf(mold, s_max(s) * c);
-      const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
-      mneg = -mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int db = 0; db < ND; ++db) o[db] *= alpha;
-      ts = exp_phase(s, c);
-    }
-    lsum += ts;
-  };
-  // O^T += V^T P^T over the 64 keys of stage buffer b.
-  auto pv_phase = [&](int b) __attribute__((always_inline)) {
-    const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
-#pragma unroll
-    for (int kj = 0; kj < 4; ++kj) {
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
-        o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
-      }
-    }
-  };
-
-  const int ntile = w.ja1 + (w.jb1 - w.jb0);
-  auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
-
-  // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-    if (t < ntile) issue(tile_of(t), t);
-  if (ntile >= 3) wait_vmem<2 * SLOTS>();
-  else if (ntile == 2) wait_vmem<SLOTS>();
-  else wait_vmem<0>();
-  barrier_lds();
-  f32x16 sa[2], sb[2];
-  if (ntile > 0) {
-    qk_phase(0, sa);
-    mask_phase(tile_of(0), sa);
-    fix_straddle(tile_of(0), sa);
-  }
-
-  // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
-  // core, then O += V P of tile it while the VALU masks S(it+1).
-  // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
-  // barrier of step it), its buffer's previous tile it-1 is finished by every
-  // wave.
-  int it = 0;
-  auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
-    const bool has_next = it + 1 < ntile;
-    if (has_next) {
-      if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
-      else wait_vmem<0>();
-      barrier_lds();
-      if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
-    }
-    // S of the next tile is computed unconditionally (on the last tile it
-    // reads a stale but complete buffer and is discarded) so that it shares a
-    // basic block with the softmax VALU work and the two interleave.
-    const float c = tile_c(tile_of(it));
-    const float ts = exp_phase(cur, c);
-    qk_phase((it + 1) & 3, nxt);
-    finish_tile(cur, ts, c);
-    pv_phase(it & 3);
-    if (has_next) {
-      mask_phase(tile_of(it + 1), nxt);
-      fix_straddle(tile_of(it + 1), nxt);
-    }
-    ++it;
-  };
-  while (it < ntile) {
-    step(sa, sb);
-    if (it < ntile) step(sb, sa);
-  }
-
-  // Epilogue: O = O^T / l, written token-major [N, H, D].
-  const float l = lsum + __shfl_xor(lsum, 32);
-  const float linv = l > 0.f ? 1.0f / l : 0.f;
-  if (!qvalid) return;
-  TOut *row = static_cast<TOut *>(p.o) + (int64_t)(sg.start + ql) * p.o_st + (int64_t)head * p.o_sh + 4 * hl;
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x4 x = {o[db][4 * r4] * linv, o[db][4 * r4 + 1] * linv, o[db][4 * r4 + 2] * linv,
-                       o[db][4 * r4 + 3] * linv};
-      store4<TOut>(row + 32 * db + 8 * r4, x);
-    }
+  }  // units
 }
 
 // ---------------------------------------------------------------- host side
@@ -818,6 +849,12 @@ int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads) {
   return dan::kWaveQ * dan::kWaves / dan::heads_per_group(num_heads / num_kv_heads);
 }
 
+int dan_tree_attn_head_groups(int32_t num_heads, int32_t num_kv_heads) {
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  const int rep = num_heads / num_kv_heads, hpw = dan::heads_per_group(rep);
+  return num_kv_heads * ((rep + hpw - 1) / hpw);
+}
+
 int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols) {
   if (num_kv_heads <= 0 || head_dim <= 0 || vt_cols < 0 || vt_cols % dan::kKeyTile) return 0;
   return (int64_t)num_kv_heads * head_dim * vt_cols * 2;
@@ -863,9 +900,12 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
     return fail(DAN_ERR_UNSUPPORTED, "k token stride %lld or vt_cols %d is too large", (long long)a->k_stride_tok, a->vt_cols);
   const int hpw = heads_per_group(rep);
   const int chunks = (rep + hpw - 1) / hpw;
-  const int64_t grid = (int64_t)a->num_work * Hkv * chunks;
+  const int64_t units = (int64_t)a->num_work * Hkv * chunks;
   const int64_t pack_grid = (int64_t)(a->vt_cols / kKeyTile) * Hkv;
-  if (grid > 0x7fffffff || pack_grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "grid is too large");
+  if (units > 0x7fffffff || pack_grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "grid is too large");
+  if (a->phases != DAN_TREE_ATTN_PHASE_PACK && (!a->sched || !a->sched_off || a->num_slots <= 0 || a->num_slots > units))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "schedule: need sched, sched_off and 1 <= num_slots <= %lld units",
+                (long long)units);
 
   PackParams pp;
   pp.v = a->v; pp.v_st = a->v_stride_tok; pp.v_sh = a->v_stride_head;
@@ -883,6 +923,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
   kp.c = a->scale * 1.4426950408889634f;
   kp.q_scale = a->q_scale; kp.k_scale = a->k_scale;
+  kp.sched = a->sched; kp.sched_off = a->sched_off; kp.num_units = (int32_t)units;
+  const int grid = a->num_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool d128 = D == 128;
@@ -896,10 +938,10 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   }
   if (a->phases == DAN_TREE_ATTN_PHASE_PACK) return DAN_OK;
 
-  if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, (int)grid, s) : launch_attn<__bf16, __bf16, 64>(kp, (int)grid, s);
-  else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, (int)grid, s) : launch_attn<_Float16, _Float16, 64>(kp, (int)grid, s);
-  else if (f8) err = d128 ? launch_attn<E4M3, __bf16, 128>(kp, (int)grid, s) : launch_attn<E4M3, __bf16, 64>(kp, (int)grid, s);
-  else err = d128 ? launch_attn<_Float16, float, 128>(kp, (int)grid, s) : launch_attn<_Float16, float, 64>(kp, (int)grid, s);
+  if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, grid, s) : launch_attn<__bf16, __bf16, 64>(kp, grid, s);
+  else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, grid, s) : launch_attn<_Float16, _Float16, 64>(kp, grid, s);
+  else if (f8) err = d128 ? launch_attn<E4M3, __bf16, 128>(kp, grid, s) : launch_attn<E4M3, __bf16, 64>(kp, grid, s);
+  else err = d128 ? launch_attn<_Float16, float, 128>(kp, grid, s) : launch_attn<_Float16, float, 64>(kp, grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
 }

@@ -108,6 +108,76 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
     return segs, work[order], key_lo, cost[order], past_dicts, np.array(col_seg, np.int32)
 
 
+def schedule(cost, groups, num_cus, overhead=1):
+    """Persistent schedule of the attention launch: (sched int32[U], sched_off
+    int32[S + 1]) for U = len(cost) * groups units, unit u = work item
+    u // groups for head group u % groups.
+
+    There are S = groups * k slots (work groups), k = min(num_cus // groups,
+    items) (at least 1), about one per CU. Slot s takes only units of head
+    group s % groups: the hardware deals work groups to the 8 XCDs round
+    robin, so with 8 kv heads each XCD's L2 serves one kv head. Inside a
+    class, items are dealt longest first to the least loaded slot (LPT),
+    each costing its key tiles plus ``overhead`` for its prologue and
+    epilogue. Every class sees the same item costs, so one assignment serves
+    all of them. dan's varlen path has no counterpart: there the flash
+    kernels' own grids decide (dan/attention.py:229-241)."""
+    import heapq
+
+    cost = np.asarray(cost, np.int64)
+    n = len(cost)
+    if n == 0 or groups <= 0:
+        return np.zeros(0, np.int32), np.zeros(1, np.int32)
+    k = max(1, min(num_cus // groups, n))
+    heap = [(0, j) for j in range(k)]
+    per = [[] for _ in range(k)]
+    for i in np.argsort(-cost, kind="stable"):
+        load, j = heapq.heappop(heap)
+        per[j].append(int(i))
+        heapq.heappush(heap, (load + int(cost[i]) + overhead, j))
+    _rebalance(per, cost + overhead)
+    for x in per:
+        x.sort(key=lambda i: (-cost[i], i))
+    lists = [[i * groups + s % groups for i in per[s // groups]] for s in range(k * groups)]
+    off = np.zeros(len(lists) + 1, np.int32)
+    off[1:] = np.cumsum([len(x) for x in lists])
+    sched = np.array([u for x in lists for u in x], np.int32)
+    return sched, off
+
+
+def _rebalance(per, w, rounds=10000):
+    """Lower the largest load of the lists ``per`` (item weights ``w``) by
+    moving one item, or swapping two, between the most loaded list and
+    another, while that strictly lowers the pair's larger load."""
+    w = np.asarray(w, np.int64)
+    loads = np.array([int(w[x].sum()) for x in per], np.int64)
+    for _ in range(rounds):
+        a = int(np.argmax(loads))
+        top = loads[a]
+        m = max(len(x) for x in per)
+        # other[b, 0] = 0 (a move), other[b, 1 + t] = weight of list b's t-th item (a swap)
+        other = np.full((len(per), m + 1), np.iinfo(np.int64).max // 4, np.int64)
+        other[:, 0] = 0
+        for b, x in enumerate(per):
+            other[b, 1:1 + len(x)] = w[x]
+        d = w[per[a]][:, None, None] - other[None]          # [items of a, b, option]: load moved a -> b
+        new = np.maximum(top - d, loads[None, :, None] + d)
+        new[(d <= 0) | (new >= top)] = np.iinfo(np.int64).max
+        new[:, a, :] = np.iinfo(np.int64).max
+        flat = int(np.argmin(new))
+        if new.flat[flat] == np.iinfo(np.int64).max:
+            return
+        ia, b, t = np.unravel_index(flat, new.shape)
+        i = per[a].pop(int(ia))
+        if t > 0:
+            j = per[b].pop(int(t) - 1)
+            per[a].append(j)
+        per[b].append(i)
+        moved = int(d[ia, b, t])
+        loads[a] -= moved
+        loads[b] += moved
+
+
 @dataclass
 class TilePlan:
     """Device-resident tables of one packed forward (see module docstring)."""
@@ -127,6 +197,7 @@ class TilePlan:
     col_seg_d: object = None
     past_tables: dict = field(default_factory=dict)  # layer -> (device bytes, keep-alive refs)
     workspace: dict = field(default_factory=dict)  # bytes -> device scratch (reused by every layer)
+    schedules: dict = field(default_factory=dict)  # (groups, CUs) -> (sched_d, sched_off_d, slots)
 
     @classmethod
     def build(cls, segments, num_tokens, tile_q, device):
@@ -148,6 +219,14 @@ class TilePlan:
         import torch
 
         return self.num_tokens == num_tokens and self.tile_q == tile_q and self.device == torch.device(device)
+
+    def schedule(self, groups, num_cus):
+        """Device copy of ``schedule(self.cost, groups, num_cus)`` (cached)."""
+        key = (groups, num_cus)
+        if key not in self.schedules:
+            sched, off = schedule(self.cost, groups, num_cus)
+            self.schedules[key] = (_upload(sched, self.device), _upload(off, self.device), len(off) - 1)
+        return self.schedules[key]
 
     def key_tiles(self):
         """Total key tiles the work list visits (per kv head and head chunk)."""

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 3
+#define DAN_TREE_ATTN_ABI_VERSION 4
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -152,6 +152,16 @@ typedef struct {
    * previous call filled for the same v and pasts) -- for callers that
    * overlap the copy with other work, and for timing each launch. */
   int32_t phases;
+  /* Persistent schedule of the attention launch: `num_slots` work groups
+   * (about one per CU), slot s processing units sched[sched_off[s]] ..
+   * sched[sched_off[s + 1] - 1] in order. Unit u is work item u / G for head
+   * group u % G, G = dan_tree_attn_head_groups(num_heads, num_kv_heads); every
+   * unit in [0, num_work * G) must appear exactly once. Slot s runs on XCD
+   * s % 8, so a planner that gives slot s only units of kv head s % Hkv keeps
+   * each kv head's keys and values in one XCD's L2. */
+  const int32_t *sched;
+  const int32_t *sched_off; /* [num_slots + 1], sched_off[0] = 0 */
+  int32_t num_slots;
 } DanTreeAttnArgs;
 
 #define DAN_TREE_ATTN_PHASES_ALL 0
@@ -170,6 +180,11 @@ int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int
  * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172).
  * Returns 0 for an unsupported configuration. */
 int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads);
+
+/* Head groups G of the schedule: kv heads times the query-head chunks one
+ * work group covers: num_kv_heads * ceil(rep / 4), rep = num_heads /
+ * num_kv_heads. Returns 0 for an unsupported configuration. */
+int dan_tree_attn_head_groups(int32_t num_heads, int32_t num_kv_heads);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char *dan_tree_attn_last_error(void);

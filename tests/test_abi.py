@@ -82,6 +82,10 @@ def test_abi_version_and_tile_q(lib):
     assert _native.tile_q(8, 8, lib) == 256   # rep 1
     assert _native.tile_q(12, 8, lib) == 0    # not a multiple
     assert _native.tile_q(0, 8, lib) == 0
+    assert _native.head_groups(32, 8, lib) == 8     # rep 4: one chunk per kv head
+    assert _native.head_groups(14, 2, lib) == 4     # rep 7: two chunks
+    assert _native.head_groups(16, 8, lib) == 8
+    assert _native.head_groups(12, 8, lib) == 0
 
 
 def _args(**kw):
@@ -149,3 +153,9 @@ def test_bad_scale_dtype_and_workspace(lib):
     ph = _args(**dict(full, phases=3))
     assert lib.dan_tree_attn_fwd(ctypes.byref(ph), None) == _native.ERR_INVALID_ARGUMENT
     assert "phases" in _native.last_error(lib)
+    # the attention launch needs a schedule of 1..units slots (1 item x 8 head groups here)
+    for sched in (dict(), dict(sched=p, sched_off=p, num_slots=0), dict(sched=p, sched_off=p, num_slots=9),
+                  dict(sched=p, num_slots=8)):
+        rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**dict(full, **sched))), None)
+        assert rc == _native.ERR_INVALID_ARGUMENT
+        assert "schedule" in _native.last_error(lib)

@@ -345,3 +345,40 @@ def test_phases_split_equals_one_call(gpu):
     torch.cuda.synchronize()
     rows = torch.cat([torch.arange(s.start, s.end) for s in w.segments])
     assert torch.equal(out[:, rows], full[:, rows])
+
+
+def test_schedule_order_is_invisible(gpu):
+    """Units are independent: the planned persistent schedule, one unit per
+    work group in natural order, one work group per head group walking all
+    of its units, and every list reversed give the same output bit for bit."""
+    from dan_amd import _native
+    from dan_amd import plan as plan_mod
+    from dan_amd.attention import _num_cus, get_plan
+    w = W.config3(0, device=gpu)
+    say("schedule variants c3")
+    ref = attend(w.q, w.k, w.v, w.segments, 0).clone()
+    h, hkv = w.q.shape[0], w.k.shape[0]
+    plan = get_plan(w.segments, w.num_tokens, _native.tile_q(h, hkv), w.q.device)
+    groups = _native.head_groups(h, hkv)
+    key = (groups, _num_cus(w.q.device))
+    planned = plan.schedules[key]
+    units = len(plan.work) * groups
+    sched, off = plan_mod.schedule(plan.cost, groups, key[1])
+    lists = [sched[off[s]:off[s + 1]] for s in range(len(off) - 1)]
+    variants = {
+        "one unit per work group": [[u] for u in range(units)],
+        "one work group per head group": [[u for u in range(units) if u % groups == g] for g in range(groups)],
+        "reversed lists": [x[::-1] for x in lists],
+    }
+    try:
+        for name, lst in variants.items():
+            say(f"schedule variant: {name}")
+            flat = np.array([u for x in lst for u in x], np.int32)
+            offs = np.zeros(len(lst) + 1, np.int32)
+            offs[1:] = np.cumsum([len(x) for x in lst])
+            plan.schedules[key] = (plan_mod._upload(flat, w.q.device), plan_mod._upload(offs, w.q.device), len(lst))
+            out = attend(w.q, w.k, w.v, w.segments, 0)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), name
+    finally:
+        plan.schedules[key] = planned

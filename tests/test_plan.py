@@ -10,7 +10,7 @@ from hypothesis import strategies as st
 
 from dan_amd import workloads as W
 from dan_amd.attention import Batch, Segment, segment
-from dan_amd.plan import KEY_TILE, build_tables, validate_segments
+from dan_amd.plan import KEY_TILE, build_tables, schedule, validate_segments
 from oracle import tree_attention as O
 
 
@@ -129,3 +129,45 @@ def test_segment_mirrors_reference_construction():
     assert (s.start, s.end, s.trunk, s.branches, s.past_len, s.save) == (7, 13, 3, [(10, 12), (12, 13)], 4, 2)
     assert segment(0, [0, 1], past=None, past_len=9).past_len == 0
     assert s.mask.shape == (3, 4 + 6) and s.mask[:, :4].all()
+
+
+def check_schedule(cost, groups, num_cus):
+    sched, off = schedule(cost, groups, num_cus)
+    slots = len(off) - 1
+    units = len(cost) * groups
+    assert off[0] == 0 and off[-1] == units and (np.diff(off) >= 0).all()
+    assert sorted(sched.tolist()) == list(range(units)), "every unit exactly once"
+    assert 1 <= slots <= max(num_cus, groups) and slots % groups == 0
+    # slot s serves head group s % groups only (one kv head per XCD)
+    for s in range(slots):
+        assert all(u % groups == s % groups for u in sched[off[s]:off[s + 1]])
+    loads = np.array([sum(int(cost[u // groups]) + 1 for u in sched[off[s]:off[s + 1]]) for s in range(slots)])
+    per_class = slots // groups
+    ideal = (int(cost.sum()) + len(cost)) / per_class
+    # a balanced assignment: within one item of the mean (or the largest item)
+    assert loads.max() <= max(ideal + int(cost.max()) + 1, int(cost.max()) + 1)
+    return sched, off, loads, ideal
+
+
+def test_schedule_balances_config3():
+    w = W.config3(0)
+    _, _, _, cost, _, _ = build_tables(w.segments, w.num_tokens, 64)
+    sched, off, loads, ideal = check_schedule(cost, 8, 256)
+    assert len(off) - 1 == 256
+    # hardware round-robin dispatch of 1040 work groups ends at 147 tile-steps on
+    # the busiest CU; the planned schedule is within 1 % of the mean
+    assert loads.max() <= 1.01 * ideal, (loads.max(), ideal)
+
+
+@settings(max_examples=40, deadline=None)
+@given(st.lists(st.integers(1, 200), min_size=1, max_size=300), st.sampled_from([1, 2, 4, 8, 16]),
+       st.sampled_from([8, 64, 256]))
+def test_schedule_random_costs(costs, groups, cus):
+    check_schedule(np.array(sorted(costs, reverse=True), np.int64), groups, cus)
+
+
+def test_schedule_fewer_items_than_cus():
+    cost = np.array([5, 3, 1], np.int64)
+    sched, off, loads, _ = check_schedule(cost, 8, 256)
+    assert len(off) - 1 == 24 and (np.diff(off) == 1).all()  # one unit per work group
+    assert len(schedule(np.zeros(0, np.int64), 8, 256)[0]) == 0
