@@ -346,10 +346,36 @@ __device__ inline void wait_vmem() {
 __device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 #define DAN_LDS __attribute__((address_space(3)))
-// One 16-byte direct load per lane into LDS: lane l writes lds + 16 * l.
+// One 16-byte direct load per lane into LDS (global_load_lds_dwordx4: lane l
+// writes lds + 16 * l; M0 holds the LDS address). Issued from inline asm:
+// the compiler's wait-count pass treats an in-flight LDS DMA it can see as an
+// LDS event of unknown order and then makes every wait on an LDS read a full
+// lgkmcnt(0), serializing the operand reads of the matrix products. The
+// stage buffers' completion is waited for explicitly (wait_vmem), and the
+// "memory" clobber keeps compiler memory accesses from moving across.
+// Uniform base address (an SGPR pair) plus a per-lane 32-bit byte offset:
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma16(const void *base, uint32_t off, const uint8_t *lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(DAN_LDS const void *)lds;
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(__builtin_amdgcn_readfirstlane(m0))
+               : "memory", "m0");
+}
+// A per-lane 64-bit address:
+__device__ inline void dma16(const void *addr, const uint8_t *lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(DAN_LDS const void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "s"(__builtin_amdgcn_readfirstlane(m0))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A wave-uniform pointer, made visibly uniform (SGPRs) for an "s" operand.
 template <typename T>
-__device__ inline void load_to_lds(const T *src, uint8_t *lds) {
-  __builtin_amdgcn_global_load_lds((const DAN_GLOBAL void *)src, (DAN_LDS void *)lds, 16, 0, 0);
+__device__ inline const T *uniform_ptr(const T *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
 // LDS layout of one of four stage buffers: K rows [64][D] (row m holds key
@@ -539,13 +565,13 @@ void tree_attn_kernel(const KParams args) {
     static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
     const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
     const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
-    auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {
+    auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
       const int pos = blk * 64 + lane;
-      return (uint32_t)(k_row(pos / KC) * st + CE * min(pos % KC, KC - 2));
+      return (uint32_t)((k_row(pos / KC) * st + CE * min(pos % KC, KC - 2)) * (int64_t)sizeof(TQK));
     };
-    auto v_offset = [&](int blk) __attribute__((always_inline)) {  // blk counts from the first V^T block
+    auto v_offset = [&](int blk) __attribute__((always_inline)) {  // bytes; blk counts from the first V^T block
       const int pos = blk * 64 + lane;
-      return (uint32_t)((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2));
+      return (uint32_t)(((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2)) * 2);
     };
     uint32_t kon[KF > 0 ? KF : 1], kop[KF > 0 ? KF : 1], von[VF > 0 ? VF : 1];  // (KF is 0 for e4m3, D = 64)
 #pragma unroll
@@ -556,7 +582,7 @@ void tree_attn_kernel(const KParams args) {
 #pragma unroll
     for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
     // last slot: K offsets (new, past) or the V^T / sink offset
-    const uint32_t sink_off = (uint32_t)((lane & 7) * 8);  // sink: any valid V^T address
+    const uint32_t sink_off = (uint32_t)((lane & 7) * 16);  // sink: any valid V^T address (bytes)
     const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
     const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
 
@@ -564,7 +590,7 @@ void tree_attn_kernel(const KParams args) {
     auto issue = [&](int j, int b) __attribute__((always_inline)) {
       const int kb = j * kKeyTile;
       uint8_t *base = smem + b * L::buf;
-      const _Float16 *vtt = vtp + kb;
+      const _Float16 *vtt = uniform_ptr(vtp + kb);
       auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
         const int pos = blk * 64 + lane;
         const int col = CE * min(pos % KC, KC - 2);
@@ -573,25 +599,25 @@ void tree_attn_kernel(const KParams args) {
       };
       // (Separate loops per source layout: a select between two offset arrays
       // would make the compiler keep them in scratch memory.)
-      if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit offsets
-        const TQK *tb = pkp + (int64_t)kb * pk_st;
+      if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit byte offsets
+        const TQK *tb = uniform_ptr(pkp + (int64_t)kb * pk_st);
 #pragma unroll
-        for (int s = 0; s < KF; ++s) load_to_lds(tb + kop[s], base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) load_to_lds(tb + lop, base + last_blk * 1024);
+        for (int s = 0; s < KF; ++s) dma16(tb, kop[s], base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) dma16(tb, lop, base + last_blk * 1024);
       } else if (kb >= P && kb + kKeyTile <= PN) {
-        const TQK *tb = kp + (int64_t)(sg.start + kb - P) * p.k_st;
+        const TQK *tb = uniform_ptr(kp + (int64_t)(sg.start + kb - P) * p.k_st);
 #pragma unroll
-        for (int s = 0; s < KF; ++s) load_to_lds(tb + kon[s], base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) load_to_lds(tb + lon, base + last_blk * 1024);
+        for (int s = 0; s < KF; ++s) dma16(tb, kon[s], base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) dma16(tb, lon, base + last_blk * 1024);
       } else {
 #pragma unroll
-        for (int s = 0; s < KF; ++s) load_to_lds(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) load_to_lds(k_slow(last_blk), base + last_blk * 1024);
+        for (int s = 0; s < KF; ++s) dma16(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
+        if (last_kind == 0) dma16(k_slow(last_blk), base + last_blk * 1024);
       }
 #pragma unroll
-      for (int s = 0; s < VF; ++s) load_to_lds(vtt + von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
-      if (last_kind == 1) load_to_lds(vtt + lon, base + last_blk * 1024);
-      if (last_kind == 2) load_to_lds(vtt + lon, smem + L::sink);
+      for (int s = 0; s < VF; ++s) dma16(vtt, von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
+      if (last_kind == 1) dma16(vtt, lon, base + last_blk * 1024);
+      if (last_kind == 2) dma16(vtt, lon, smem + L::sink);
     };
 
     f32x16 o[ND];
@@ -739,7 +765,11 @@ void tree_attn_kernel(const KParams args) {
     const int ntile = w.ja1 + (w.jb1 - w.jb0);
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
-    // Prologue: tiles 0..2 in flight, wait for tile 0, score it.
+    // Prologue: tiles 0..2 in flight, wait for tile 0, score it. The
+    // compiler does not see the direct loads, so its own loads (q, the own
+    // key, key_lo) are waited for first: a wait it placed for them later
+    // (vmcnt(0) by its count) would also drain the tiles in flight.
+    wait_vmem<0>();
 #pragma unroll
     for (int t = 0; t < 3; ++t)
       if (t < ntile) issue(tile_of(t), t);
