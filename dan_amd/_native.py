@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 KEY_TILE = 64
 
 # DanStatus
@@ -48,6 +48,11 @@ class DanWorkItem(ctypes.Structure):
                 ("jfull", _i32), ("lo_max", _i32)]
 
 
+class DanUnit(ctypes.Structure):
+    _fields_ = [("item", DanWorkItem), ("start", _i32), ("n", _i32), ("trunk", _i32), ("past_len", _i32),
+                ("past_idx", _i32), ("vt_col", _i32), ("group", _i32), ("reserved", _i32)]
+
+
 class DanTreeAttnArgs(ctypes.Structure):
     _fields_ = [("abi_version", _i32), ("in_dtype", _i32), ("out_dtype", _i32), ("v_dtype", _i32),
                 ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("num_tokens", _i32),
@@ -64,7 +69,7 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("tile_q", _i32), ("vt_cols", _i32),
                 ("col_seg", _vp),
                 ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32),
-                ("sched", _vp), ("sched_off", _vp), ("num_slots", _i32)]
+                ("units", _vp), ("sched_off", _vp), ("num_slots", _i32)]
 
 
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",

@@ -314,7 +314,7 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
             a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
         a.phases = phases
         groups = _native.head_groups(h, hkv, lib)
-        sched, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
-        a.sched, a.sched_off, a.num_slots = sched.data_ptr(), sched_off.data_ptr(), slots
+        units, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
+        a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

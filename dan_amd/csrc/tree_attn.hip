@@ -105,19 +105,17 @@ struct KParams {
   void *o;
   const _Float16 *vt;
   int64_t q_st, q_sh, k_st, k_sh, o_st, o_sh;
-  const DanSegmentDesc *segs;
   const DanPastDesc *pasts;
-  const DanWorkItem *work;
   const int32_t *key_lo;
   int32_t num_kv_heads, rep, hpw, chunks, vt_cols;
   float c;  // softmax scale * log2(e)
   // e4m3 only: per-tensor scales of q and k (device fp32 scalars); S is
   // scaled by q_scale * k_scale (a prefix-cache entry has its own k scale).
   const float *q_scale, *k_scale;
-  // Persistent schedule: work group b runs units sched[sched_off[b]] ..
-  // sched[sched_off[b + 1] - 1]; unit u = work item u / groups, head group
-  // u % groups.
-  const int32_t *sched, *sched_off;
+  // Persistent schedule: work group b runs units[sched_off[b]] ..
+  // units[sched_off[b + 1] - 1] (work items with their segment's fields).
+  const DanUnit *units;
+  const int32_t *sched_off;
   int32_t num_units;
 };
 
@@ -159,6 +157,21 @@ __device__ inline T load_entry(const T *p) {
   const DAN_GLOBAL uint32_t *src = gbl(reinterpret_cast<const uint32_t *>(p));
 #pragma unroll
   for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = src[i];
+  return __builtin_bit_cast(T, raw);
+}
+
+// The same for an entry every lane reads at the same address: each dword is
+// made visibly wave-uniform (SGPRs), so control flow that depends on it stays
+// scalar.
+template <typename T>
+__device__ inline T load_uniform(const T *p) {
+  static_assert(sizeof(T) % 4 == 0, "table entries are dword multiples");
+  struct Raw {
+    uint32_t w[sizeof(T) / 4];
+  } raw;
+  const DAN_GLOBAL uint32_t *src = gbl(reinterpret_cast<const uint32_t *>(p));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
   return __builtin_bit_cast(T, raw);
 }
 
@@ -482,7 +495,7 @@ void tree_attn_kernel(const KParams args) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, lq = lane & 31;
 
-  // sched holds num_units entries: clamping the range keeps a malformed
+  // units holds num_units records: clamping the range keeps a malformed
   // offset table from reading past it.
   const int u_begin = max(*gbl(args.sched_off + blockIdx.x), 0);
   const int u_end = min(*gbl(args.sched_off + blockIdx.x + 1), args.num_units);
@@ -497,15 +510,17 @@ void tree_attn_kernel(const KParams args) {
     asm volatile("" : "+s"(kp_u));
     const KParams &p = *(const KParams *)kp_u;
     const int groups = p.num_kv_heads * p.chunks;
-    const int unit = __builtin_amdgcn_readfirstlane(*gbl(p.sched + u));
-    if (unit < 0 || unit >= p.num_units) continue;  // a malformed schedule entry: skip it
+    const DanUnit un = load_uniform(p.units + u);  // one read resolves the unit
+    const int g = un.group;
+    if (g < 0 || g >= groups) continue;  // a malformed unit record: skip it
     // Every wave is done with the previous unit's stage buffers before this
     // unit's first tiles are loaded into them.
     barrier_lds();
-    const DanWorkItem w = load_entry(p.work + unit / groups);
-    const int g = unit % groups;
+    const DanWorkItem &w = un.item;
     const int kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
-    const DanSegmentDesc sg = load_entry(p.segs + w.seg);
+    struct {
+      int start, n, trunk, past_len, past_idx, vt_col;
+    } const sg = {un.start, un.n, un.trunk, un.past_len, un.past_idx, un.vt_col};
     const int P = sg.past_len, PT = P + sg.trunk, PN = P + sg.n;
     const int H = p.num_kv_heads * p.rep;
 
@@ -537,13 +552,7 @@ void tree_attn_kernel(const KParams args) {
     const bool qvalid = wave_work && ql < qend;
     const int qrow = sg.start + min(ql, qend - 1);
     const int qk = qvalid ? P + ql : 0x3fffffff;
-    const int qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
-    Frag<TQK> qf[NK];
-    {
-      const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
-    }
+    Frag<TQK> qf[NK];  // loaded after the first tiles' direct loads are issued
     // Raw score of the query against its own key (key coordinate P + query,
     // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
     auto self_score = [&](const Frag<TQK>(&q)[NK], int qr) __attribute__((always_inline)) {
@@ -623,9 +632,8 @@ void tree_attn_kernel(const KParams args) {
     f32x16 o[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
-    // Exponent offset -m of the running max m, which starts at the query's
-    // score against its own key (always visible to it).
-    float mneg = -self_score(qf, qrow) * c_new, lsum = 0.f;
+    float mneg, lsum = 0.f;  // exponent offset -m of the running max m
+    int qlo;
     u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
     // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
@@ -765,17 +773,25 @@ void tree_attn_kernel(const KParams args) {
     const int ntile = w.ja1 + (w.jb1 - w.jb0);
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
-    // Prologue: tiles 0..2 in flight, wait for tile 0, score it. The
-    // compiler does not see the direct loads, so its own loads (q, the own
-    // key, key_lo) are waited for first: a wait it placed for them later
-    // (vmcnt(0) by its count) would also drain the tiles in flight.
+    // Prologue: tiles 0..2 in flight; meanwhile load q, key_lo and the
+    // query's own key. The running max m starts at the query's score against
+    // its own key (always visible to it). The compiler does not see the
+    // direct loads, so every load of its own is complete before they are
+    // issued: it waits for its loads by its own count, so a wait it placed
+    // for an earlier load would also drain the tiles in flight, and its
+    // waits for the loads below drain them anyway (tile 0 is needed next).
     wait_vmem<0>();
 #pragma unroll
     for (int t = 0; t < 3; ++t)
       if (t < ntile) issue(tile_of(t), t);
-    if (ntile >= 3) wait_vmem<2 * SLOTS>();
-    else if (ntile == 2) wait_vmem<SLOTS>();
-    else wait_vmem<0>();
+    qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
+    {
+      const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
+    }
+    mneg = -self_score(qf, qrow) * c_new;
+    wait_vmem<0>();
     barrier_lds();
     f32x16 sa[2], sb[2];
     if (ntile > 0) {
@@ -933,8 +949,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   const int64_t units = (int64_t)a->num_work * Hkv * chunks;
   const int64_t pack_grid = (int64_t)(a->vt_cols / kKeyTile) * Hkv;
   if (units > 0x7fffffff || pack_grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "grid is too large");
-  if (a->phases != DAN_TREE_ATTN_PHASE_PACK && (!a->sched || !a->sched_off || a->num_slots <= 0 || a->num_slots > units))
-    return fail(DAN_ERR_INVALID_ARGUMENT, "schedule: need sched, sched_off and 1 <= num_slots <= %lld units",
+  if (a->phases != DAN_TREE_ATTN_PHASE_PACK && (!a->units || !a->sched_off || a->num_slots <= 0 || a->num_slots > units))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "schedule: need units, sched_off and 1 <= num_slots <= %lld units",
                 (long long)units);
 
   PackParams pp;
@@ -949,11 +965,11 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   kp.q_st = a->q_stride_tok; kp.q_sh = a->q_stride_head;
   kp.k_st = a->k_stride_tok; kp.k_sh = a->k_stride_head;
   kp.o_st = a->o_stride_tok; kp.o_sh = a->o_stride_head;
-  kp.segs = a->segments; kp.pasts = a->pasts; kp.work = a->work; kp.key_lo = a->key_lo;
+  kp.pasts = a->pasts; kp.key_lo = a->key_lo;
   kp.num_kv_heads = Hkv; kp.rep = rep; kp.hpw = hpw; kp.chunks = chunks; kp.vt_cols = a->vt_cols;
   kp.c = a->scale * 1.4426950408889634f;
   kp.q_scale = a->q_scale; kp.k_scale = a->k_scale;
-  kp.sched = a->sched; kp.sched_off = a->sched_off; kp.num_units = (int32_t)units;
+  kp.units = a->units; kp.sched_off = a->sched_off; kp.num_units = (int32_t)units;
   const int grid = a->num_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);

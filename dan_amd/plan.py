@@ -178,6 +178,20 @@ def _rebalance(per, w, rounds=10000):
         loads[b] += moved
 
 
+def unit_records(segs, work, sched, groups):
+    """The attention launch's unit table in schedule order: int32 [U, 16]
+    rows laid out as DanUnit -- the work item (8 fields), its segment's start,
+    n, trunk, past_len, past_idx, vt_col, the head group, and 0."""
+    sched = np.asarray(sched, np.int64)
+    rec = np.zeros((len(sched), 16), np.int32)
+    if len(sched):
+        items = work[sched // groups]
+        rec[:, :8] = items
+        rec[:, 8:14] = segs[items[:, 0], :6]
+        rec[:, 14] = sched % groups
+    return rec
+
+
 @dataclass
 class TilePlan:
     """Device-resident tables of one packed forward (see module docstring)."""
@@ -197,7 +211,7 @@ class TilePlan:
     col_seg_d: object = None
     past_tables: dict = field(default_factory=dict)  # layer -> (device bytes, keep-alive refs)
     workspace: dict = field(default_factory=dict)  # bytes -> device scratch (reused by every layer)
-    schedules: dict = field(default_factory=dict)  # (groups, CUs) -> (sched_d, sched_off_d, slots)
+    schedules: dict = field(default_factory=dict)  # (groups, CUs) -> (units_d, sched_off_d, slots)
 
     @classmethod
     def build(cls, segments, num_tokens, tile_q, device):
@@ -221,11 +235,13 @@ class TilePlan:
         return self.num_tokens == num_tokens and self.tile_q == tile_q and self.device == torch.device(device)
 
     def schedule(self, groups, num_cus):
-        """Device copy of ``schedule(self.cost, groups, num_cus)`` (cached)."""
+        """Device copies of the unit records of ``schedule(self.cost, groups,
+        num_cus)`` and of its slot offsets, and the slot count (cached)."""
         key = (groups, num_cus)
         if key not in self.schedules:
             sched, off = schedule(self.cost, groups, num_cus)
-            self.schedules[key] = (_upload(sched, self.device), _upload(off, self.device), len(off) - 1)
+            units = unit_records(self.segs, self.work, sched, groups)
+            self.schedules[key] = (_upload(units, self.device), _upload(off, self.device), len(off) - 1)
         return self.schedules[key]
 
     def key_tiles(self):

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 4
+#define DAN_TREE_ATTN_ABI_VERSION 5
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -108,6 +108,21 @@ typedef struct {
   int32_t lo_max;
 } DanWorkItem;
 
+/* One unit of the attention launch's persistent schedule: a work item for one
+ * head group, with its segment's fields copied in, so that a work group
+ * resolves a unit with a single 64-byte read. */
+typedef struct {
+  DanWorkItem item;
+  int32_t start;    /* the item's segment: DanSegmentDesc.start */
+  int32_t n;        /* .n */
+  int32_t trunk;    /* .trunk */
+  int32_t past_len; /* .past_len */
+  int32_t past_idx; /* .past_idx */
+  int32_t vt_col;   /* .vt_col */
+  int32_t group;    /* head group: kv head + num_kv_heads * chunk, in [0, G) */
+  int32_t reserved;
+} DanUnit;
+
 typedef struct {
   int32_t abi_version; /* DAN_TREE_ATTN_ABI_VERSION */
   int32_t in_dtype;    /* DanDtype of q, k and the pasts' k: bf16, f16 or e4m3 */
@@ -153,13 +168,15 @@ typedef struct {
    * overlap the copy with other work, and for timing each launch. */
   int32_t phases;
   /* Persistent schedule of the attention launch: `num_slots` work groups
-   * (about one per CU), slot s processing units sched[sched_off[s]] ..
-   * sched[sched_off[s + 1] - 1] in order. Unit u is work item u / G for head
-   * group u % G, G = dan_tree_attn_head_groups(num_heads, num_kv_heads); every
-   * unit in [0, num_work * G) must appear exactly once. Slot s runs on XCD
-   * s % 8, so a planner that gives slot s only units of kv head s % Hkv keeps
-   * each kv head's keys and values in one XCD's L2. */
-  const int32_t *sched;
+   * (about one per CU), slot s processing units[sched_off[s]] ..
+   * units[sched_off[s + 1] - 1] in order. `units` holds num_work * G records,
+   * G = dan_tree_attn_head_groups(num_heads, num_kv_heads): every (work item,
+   * head group) pair exactly once. Slot s runs on XCD s % 8, so a planner
+   * that gives slot s only units of kv head s % Hkv keeps each kv head's keys
+   * and values in one XCD's L2. The attention launch reads the work items
+   * and segments through `units`; `work` and `segments` keep their meaning
+   * for the V^T copy and for validation. */
+  const DanUnit *units;
   const int32_t *sched_off; /* [num_slots + 1], sched_off[0] = 0 */
   int32_t num_slots;
 } DanTreeAttnArgs;

@@ -40,6 +40,7 @@ def test_exports_every_declared_function(lib):
 
 
 STRUCTS = {
+    "DanUnit": _native.DanUnit,
     "DanSegmentDesc": _native.DanSegmentDesc,
     "DanPastDesc": _native.DanPastDesc,
     "DanWorkItem": _native.DanWorkItem,
@@ -154,8 +155,8 @@ def test_bad_scale_dtype_and_workspace(lib):
     assert lib.dan_tree_attn_fwd(ctypes.byref(ph), None) == _native.ERR_INVALID_ARGUMENT
     assert "phases" in _native.last_error(lib)
     # the attention launch needs a schedule of 1..units slots (1 item x 8 head groups here)
-    for sched in (dict(), dict(sched=p, sched_off=p, num_slots=0), dict(sched=p, sched_off=p, num_slots=9),
-                  dict(sched=p, num_slots=8)):
+    for sched in (dict(), dict(units=p, sched_off=p, num_slots=0), dict(units=p, sched_off=p, num_slots=9),
+                  dict(units=p, num_slots=8)):
         rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**dict(full, **sched))), None)
         assert rc == _native.ERR_INVALID_ARGUMENT
         assert "schedule" in _native.last_error(lib)

@@ -376,7 +376,8 @@ def test_schedule_order_is_invisible(gpu):
             flat = np.array([u for x in lst for u in x], np.int32)
             offs = np.zeros(len(lst) + 1, np.int32)
             offs[1:] = np.cumsum([len(x) for x in lst])
-            plan.schedules[key] = (plan_mod._upload(flat, w.q.device), plan_mod._upload(offs, w.q.device), len(lst))
+            units = plan_mod.unit_records(plan.segs, plan.work, flat, groups)
+            plan.schedules[key] = (plan_mod._upload(units, w.q.device), plan_mod._upload(offs, w.q.device), len(lst))
             out = attend(w.q, w.k, w.v, w.segments, 0)
             torch.cuda.synchronize()
             assert torch.equal(out, ref), name

@@ -10,7 +10,7 @@ from hypothesis import strategies as st
 
 from dan_amd import workloads as W
 from dan_amd.attention import Batch, Segment, segment
-from dan_amd.plan import KEY_TILE, build_tables, schedule, validate_segments
+from dan_amd.plan import KEY_TILE, build_tables, schedule, unit_records, validate_segments
 from oracle import tree_attention as O
 
 
@@ -147,6 +147,20 @@ def check_schedule(cost, groups, num_cus):
     # a balanced assignment: within one item of the mean (or the largest item)
     assert loads.max() <= max(ideal + int(cost.max()) + 1, int(cost.max()) + 1)
     return sched, off, loads, ideal
+
+
+def test_unit_records_resolve_items_and_segments():
+    w = W.config3(0)
+    segs, work, _, cost, _, _ = build_tables(w.segments, w.num_tokens, 64)
+    sched, off = schedule(cost, 8, 256)
+    rec = unit_records(segs, work, sched, 8)
+    assert rec.shape == (len(work) * 8, 16) and rec.dtype == np.int32
+    for r, u in zip(rec, sched):
+        item = work[u // 8]
+        assert (r[:8] == item).all()
+        assert (r[8:14] == segs[item[0], :6]).all()  # start, n, trunk, past_len, past_idx, vt_col
+        assert r[14] == u % 8 and r[15] == 0
+    assert unit_records(segs, work, np.zeros(0, np.int32), 8).shape == (0, 16)
 
 
 def test_schedule_balances_config3():
