@@ -318,12 +318,6 @@ __device__ inline float dot_frag<E4M3>(const Frag<E4M3> &a, const Frag<E4M3> &b,
   return acc;
 }
 
-// 16-bit element `e` (0..7) of a 16-byte vector, as the low half of a dword.
-__device__ inline uint32_t half_of(u32x4 v, int e) {
-  const uint32_t d = v[e >> 1];
-  return (e & 1) ? (d >> 16) : (d & 0xffffu);
-}
-
 // LDS row of key `r` (0..63) in the K tile: bits 2 and 3 swapped, which makes
 // the S^T accumulator of lane l, register i hold key 16*(i/8) + 8*(l/32) + i%8
 // of its 32-key block -- exactly the k-order of the P^T B operand.
@@ -434,9 +428,12 @@ __device__ inline u32x4 load8_v<E4M3>(const E4M3 *p, float scale) {
 template <typename TV, int D>
 __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   constexpr bool kF8 = std::is_same<TV, E4M3>::value;
-  constexpr int CPR = D / 8;
-  constexpr int KPP = 256 / CPR;  // keys per load pass
-  __shared__ __attribute__((aligned(16))) uint16_t tile[D][kKeyTile + 8];
+  constexpr int kPasses = D / 64;  // (8-value d chunk, key pair) items per thread
+  // tile: row d = 32 dwords, dword kp holding keys 2 kp and 2 kp + 1 (fp16) at
+  // position kp ^ 4 * ((d / 8) % 8). The swizzle keeps every 16-byte group of
+  // a row together and makes both phases conflict-free: each half-wave writes
+  // 8 d chunks x 4 key pairs to 32 distinct banks, and 8 lanes read one row.
+  __shared__ __attribute__((aligned(16))) uint32_t tile[D * 32];
   const int kvh = blockIdx.x % p.num_kv_heads, cb = blockIdx.x / p.num_kv_heads;
   const DanSegmentDesc sg = load_entry(p.segs + *gbl(p.col_seg + cb));
   const int key0 = cb * kKeyTile - sg.vt_col;
@@ -452,24 +449,42 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     pv_st = pd.v_stride_tok;
     if (kF8) pvs = *gbl(pd.v_scale);
   }
-  const int c = threadIdx.x % CPR;
-#pragma unroll
-  for (int pass = 0; pass < kKeyTile / KPP; ++pass) {
-    const int kr = pass * KPP + threadIdx.x / CPR;
-    const int key = key0 + kr;
+  // 8 values of key `key` (segment key coordinates) from d chunk c, as fp16.
+  auto row8 = [&](int key, int c) __attribute__((always_inline)) {
     u32x4 x = {0, 0, 0, 0};
     if (key < PN)
       x = key < P ? load8_v<TV>(pvp + (int64_t)key * pv_st + 8 * c, pvs)
                   : load8_v<TV>(vp + (int64_t)(sg.start + key - P) * p.v_st + 8 * c, vs);
+    return x;
+  };
+  const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;  // half-wave, lane in it
+  const int c_lo = j >> 2, kp_lo = j & 3;
+  u32x4 r0[kPasses], r1[kPasses];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) tile[8 * c + e][kr] = (uint16_t)half_of(x, e);
+  for (int pass = 0; pass < kPasses; ++pass) {  // all loads in flight first
+    const int item = hw + 8 * pass;
+    const int c = c_lo + 8 * (item / 8), kp = kp_lo + 4 * (item % 8);
+    r0[pass] = row8(key0 + 2 * kp, c);
+    r1[pass] = row8(key0 + 2 * kp + 1, c);
+  }
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int item = hw + 8 * pass;
+    const int c = c_lo + 8 * (item / 8), kp = kp_lo + 4 * (item % 8);
+    const f16x8 a = __builtin_bit_cast(f16x8, r0[pass]), b = __builtin_bit_cast(f16x8, r1[pass]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const f16x2 pr = {a[e], b[e]};
+      tile[(8 * c + e) * 32 + (kp ^ (4 * c_lo))] = __builtin_bit_cast(uint32_t, pr);
+    }
   }
   __syncthreads();
   _Float16 *dst = p.vt + (int64_t)kvh * D * p.vt_cols + (int64_t)cb * kKeyTile;
+#pragma unroll
   for (int i = threadIdx.x; i < D * 8; i += 256) {
-    const int d = i >> 3, ch = i & 7;
-    *gbl_mut(reinterpret_cast<u32x4 *>(dst + (int64_t)d * p.vt_cols + 8 * ch)) =
-        *reinterpret_cast<const u32x4 *>(&tile[d][8 * ch]);
+    const int d = i >> 3, q = i & 7;  // row d, keys 8 q .. 8 q + 7
+    *gbl_mut(reinterpret_cast<u32x4 *>(dst + (int64_t)d * p.vt_cols + 8 * q)) =
+        *reinterpret_cast<const u32x4 *>(&tile[d * 32 + 4 * (q ^ ((d >> 3) & 7))]);
   }
 }
 
