@@ -827,7 +827,11 @@ void tree_attn_kernel(const KParams args) {
         if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
         else wait_vmem<0>();
         barrier_lds();
-        if (it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+        // Waves 0-3 issue tile it+3's direct loads now, their SIMD partners
+        // (waves 4-7) after their softmax and S products below: the loads
+        // queue at the CU's address unit, and a wave waiting to issue them
+        // then has a partner that computes meanwhile.
+        if (wave < 4 && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
       }
       // S of the next tile is computed unconditionally (on the last tile it
       // reads a stale but complete buffer and is discarded) so that it shares a
@@ -836,6 +840,7 @@ void tree_attn_kernel(const KParams args) {
       const float ts = exp_phase(cur, c);
       qk_phase((it + 1) & 3, nxt);
       finish_tile(cur, ts, c);
+      if (wave >= 4 && has_next && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
       pv_phase(it & 3);
       if (has_next) {
         mask_phase(tile_of(it + 1), nxt);
