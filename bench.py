@@ -104,6 +104,65 @@ def copy_calibration(mib, steps):
     print(json.dumps({"copy_bytes": n, "copies": steps}), flush=True)
 
 
+FRONT_SHAPES = {
+    # name: (tokens, q heads, kv heads, head_dim, rotary dims, q/k norm)
+    "c3": (8192, 32, 8, 128, 128, None),        # Llama-3-8B: full RoPE, no q/k norm
+    "c4": (8192, 32, 8, 128, 128, "rms"),       # Qwen3-4B-style: per-head RMSNorm on q and k
+}
+
+
+def bench_front(args):
+    """The attention front end (dan_amd.front.qkv_front) on the named shape:
+    one step = one launch over q and k of a fused projection output,
+    HBM-bound; the metric is algorithmic GB/s against 8 TB/s."""
+    from dan_amd.front import qkv_front
+    n, h, hkv, d, r, norm = FRONT_SHAPES[args.workload]
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(args.seed)
+    qkv = torch.randn(n, (h + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(dev)
+    qx, kx, vx = qkv.split([h * d, hkv * d, hkv * d], dim=-1)
+    q, k, v = qx.reshape(n, h, d), kx.reshape(n, hkv, d), vx.reshape(n, hkv, d)
+    pos = torch.arange(n, dtype=torch.float32)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, r, 2, dtype=torch.float64) / r)).float()
+    ang = torch.cat((pos[:, None] * inv[None, :],) * 2, dim=-1)
+    cos, sin = ang.cos().to(torch.bfloat16).to(dev), ang.sin().to(torch.bfloat16).to(dev)
+    w = torch.ones(d, dtype=torch.bfloat16, device=dev)
+    call = lambda: qkv_front(q, k, v, cos, sin, q_norm_weight=w, k_norm_weight=w, norm=norm)
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        for _ in range(10):
+            call()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        call()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record(stream)
+        call()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    ms = [a.elapsed_time(b) for a, b in ev]
+    k_avg = statistics.mean(ms)
+    nbytes = 2 * (n * h * d + n * hkv * d) * 2 + 2 * n * r * 2  # read q, k and cos, sin; write q, k
+    gbps = nbytes / (k_avg * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "attention front end (q/k norm + RoPE + layout) algorithmic GB/s, 1 GPU",
+        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"front-{args.workload}: {n} tokens, {h}/{hkv} heads, head_dim {d}, rotary {r}, "
+                               f"q/k norm {norm}", "seed": args.seed},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_GBPS, 4), "traffic": None, "kernel_ms_avg": round(k_avg, 4),
+                     "kernel_ms_median": round(statistics.median(ms), 4), "algorithmic_mb": round(nbytes / 1e6, 2)},
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +174,9 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=300.0,
                     help="untimed calls of the same workload before the warm-up steps, until this much wall "
                          "time has passed: the GPU's clock ramps up over the first ~100 calls")
+    ap.add_argument("--front", action="store_true",
+                    help="measure the attention front end (q/k norm + RoPE + layout) on --workload c3 or c4 "
+                         "instead of the attention")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, run --steps plain device copies of this many MiB (the calibration "
                          "kernel for the HBM byte counters)")
@@ -129,6 +191,12 @@ def main():
 
     if args.copy_mib:
         copy_calibration(args.copy_mib, args.steps)
+        return
+    if args.front:
+        if args.workload not in FRONT_SHAPES:
+            print(f"--front measures {list(FRONT_SHAPES)}", file=sys.stderr)
+            sys.exit(2)
+        bench_front(args)
         return
 
     from dan_amd import _native, workloads

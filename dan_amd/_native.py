@@ -72,8 +72,29 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("units", _vp), ("sched_off", _vp), ("num_slots", _i32)]
 
 
+FRONT_ABI_VERSION = 1
+FRONT_NORM_NONE, FRONT_NORM_RMS, FRONT_NORM_RMS_ZERO_CENTERED = 0, 1, 2
+
+
+class DanFrontSave(ctypes.Structure):
+    _fields_ = [("start", _i32), ("len", _i32), ("k_dst", _vp), ("v_dst", _vp)]
+
+
+class DanQkvFrontArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("dtype", _i32), ("num_tokens", _i32), ("num_heads", _i32),
+                ("num_kv_heads", _i32), ("head_dim", _i32), ("rotary_dim", _i32), ("norm", _i32), ("eps", _f32),
+                ("q", _vp), ("q_stride_tok", _i64), ("q_stride_head", _i64),
+                ("k", _vp), ("k_stride_tok", _i64), ("k_stride_head", _i64),
+                ("v", _vp), ("v_stride_tok", _i64), ("v_stride_head", _i64),
+                ("cos", _vp), ("sin", _vp), ("cs_stride_tok", _i64),
+                ("q_norm_weight", _vp), ("k_norm_weight", _vp),
+                ("q_out", _vp), ("qo_stride_tok", _i64), ("qo_stride_head", _i64),
+                ("k_out", _vp), ("ko_stride_tok", _i64), ("ko_stride_head", _i64),
+                ("save_of", _vp), ("saves", _vp), ("num_saves", _i32)]
+
+
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
-           "dan_tree_attn_last_error", "dan_tree_attn_abi_version")
+           "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -103,9 +124,14 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_last_error.restype = ctypes.c_char_p
         lib.dan_tree_attn_abi_version.argtypes = []
         lib.dan_tree_attn_abi_version.restype = ctypes.c_int
+        lib.dan_qkv_front.argtypes = [ctypes.POINTER(DanQkvFrontArgs), _vp]
+        lib.dan_qkv_front.restype = ctypes.c_int
+        lib.dan_qkv_front_abi_version.argtypes = []
+        lib.dan_qkv_front_abi_version.restype = ctypes.c_int
         got = lib.dan_tree_attn_abi_version()
-        if got != ABI_VERSION:
-            raise RuntimeError(f"{path} speaks ABI {got}, this package {ABI_VERSION}; rebuild it")
+        if got != ABI_VERSION or lib.dan_qkv_front_abi_version() != FRONT_ABI_VERSION:
+            raise RuntimeError(f"{path} speaks ABI {got} / front end {lib.dan_qkv_front_abi_version()}, this package "
+                               f"{ABI_VERSION} / {FRONT_ABI_VERSION}; rebuild it")
         if path == LIB_PATH:
             _lib = lib
         return lib
@@ -137,3 +163,11 @@ def forward(args, stream, lib=None):
     rc = lib.dan_tree_attn_fwd(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_tree_attn_fwd failed (status {rc}): {last_error(lib)}")
+
+
+def front(args, stream, lib=None):
+    """Launch the attention front end; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_qkv_front(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_qkv_front failed ({rc}): {last_error(lib)}")

@@ -129,7 +129,7 @@ _DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_F16,
            E4M3: _native.DTYPE_E4M3}
 
 
-def attend(q, k, v, segments, layer, scale=None, *, q_scale=None, k_scale=None, v_scale=None):
+def attend(q, k, v, segments, layer, scale=None, *, q_scale=None, k_scale=None, v_scale=None, save=True):
     """q: [H, N, D]; k, v: [Hkv, N, D] (rotary applied). Returns [H, N, D]
     (dan/attention.py:200-207).
 
@@ -144,9 +144,12 @@ def attend(q, k, v, segments, layer, scale=None, *, q_scale=None, k_scale=None, 
     fp32 scales in ``q_scale``, ``k_scale``, ``v_scale`` (one-element device
     tensors). The output is bf16. An e4m3 prefix-cache entry is
     ``past[layer] = (k, v, k_scale, v_scale)``; a saving segment keeps the
-    same four-tuple."""
+    same four-tuple.
+
+    ``save=False`` skips the clones, for a caller whose front end already
+    filled ``saved[layer]`` (``dan_amd.front.qkv_front``)."""
     fp8 = q.dtype == E4M3
-    for s in segments:
+    for s in segments if save else ():
         if s.save:
             kv = (k[:, s.start:s.start + s.save].clone(), v[:, s.start:s.start + s.save].clone())
             s.saved[layer] = kv + (k_scale.clone(), v_scale.clone()) if fp8 and k_scale is not None else kv

@@ -1,0 +1,232 @@
+// Attention front end for gfx950 (MI355X, CDNA4): per-head RMSNorm and
+// rotate-half RoPE of q and k, written token-major for the tree-attention
+// kernel, with the prefix-cache rows of saving segments copied out in the
+// same pass. One launch replaces the eager chain of dan/models/llama.py:78-86
+// (dan/models/qwen3_5.py:318-326 for zero-centered norms and a partial
+// rotary) and the clones of dan/attention.py:202-204.
+//
+// Work decomposition: a head vector (one token, one head: D values, 2 D
+// bytes) is handled by D / 8 consecutive lanes, 16 bytes each; a work group
+// of 256 threads takes 256 / (D / 8) consecutive vectors of the flattened
+// [token][q heads, then kv heads] order, so q and k rows are read and written
+// as whole 256-byte (D = 128) lines. The row's sum of squares is a butterfly
+// over those lanes; the rotate-half partner of a lane's 8 values sits R / 16
+// lanes away (R = rotary dims) and is fetched with a lane permute.
+//
+// Numerics are those of the eager torch ops the reference runs: fp32
+// arithmetic, each op's result rounded to the storage type (RNE):
+//   RMS:            n = rnd(w * rnd(x * r)),   r = 1 / sqrt(sum(x^2) / D + eps)
+//   zero-centered:  n = rnd(x * r * (1 + w))
+//   rotate-half:    o = rnd(rnd(n * cos) + rnd(rot(n) * sin)),
+//                   rot(n)[i] = -n[i + R/2] for i < R/2, n[i - R/2] for R/2 <= i < R
+// The only difference from torch is the summation order of sum(x^2).
+//
+// The kernel is HBM-bound: it reads q, k (and the saved v rows) and cos /
+// sin once and writes q, k (and the saves) once.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dan_qkv_front.h"
+
+namespace dan {
+int fail(int status, const char *fmt, ...);  // tree_attn.hip: sets the thread's last-error message
+extern thread_local char g_err[512];
+}  // namespace dan
+
+namespace dan_front {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+#define DAN_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<__bf16> {
+  typedef bf16x8 type;
+};
+template <>
+struct Vec8<_Float16> {
+  typedef f16x8 type;
+};
+
+// 8 stored values (16 bytes) <-> 8 fp32 values; fp32 -> storage is RNE.
+template <typename T>
+__device__ inline f32x8 to_f32(u32x4 raw) {
+  return __builtin_convertvector(__builtin_bit_cast(typename Vec8<T>::type, raw), f32x8);
+}
+template <typename T>
+__device__ inline u32x4 from_f32(f32x8 x) {
+  return __builtin_bit_cast(u32x4, __builtin_convertvector(x, typename Vec8<T>::type));
+}
+// The result of one eager op: an fp32 value rounded to the storage type.
+template <typename T>
+__device__ inline float rnd(float x) {
+  return (float)(T)x;
+}
+
+template <typename T>
+__device__ inline u32x4 load16(const T *p) {
+  return *(const DAN_GLOBAL u32x4 *)p;
+}
+template <typename T>
+__device__ inline void store16(T *p, u32x4 v) {
+  *(DAN_GLOBAL u32x4 *)p = v;
+}
+
+struct Params {
+  const void *q, *k, *v, *cos, *sin, *qw, *kw;
+  void *qo, *ko;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, cs_st, qo_st, qo_sh, ko_st, ko_sh;
+  const int32_t *save_of;
+  const DanFrontSave *saves;
+  int32_t N, H, Hkv, R, norm;
+  float eps;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
+  constexpr int L = D / 8;      // lanes per head vector
+  constexpr int VPB = 256 / L;  // head vectors per work group
+  const int slot = threadIdx.x / L, j = threadIdx.x % L;
+  const int HV = p.H + p.Hkv;
+  const int64_t vi = (int64_t)blockIdx.x * VPB + slot;
+  // Whole vectors (all L lanes of one) leave together, so the lane
+  // exchanges below only ever involve lanes of a live vector.
+  if (vi >= (int64_t)p.N * HV) return;
+  const int t = (int)(vi / HV), hv = (int)(vi % HV);
+  const bool isq = hv < p.H;
+  const int head = isq ? hv : hv - p.H;
+  const T *src = isq ? static_cast<const T *>(p.q) + t * p.q_st + head * p.q_sh
+                     : static_cast<const T *>(p.k) + t * p.k_st + head * p.k_sh;
+  const f32x8 x = to_f32<T>(load16(src + 8 * j));
+
+  f32x8 n = x;
+  if (p.norm != DAN_FRONT_NORM_NONE) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+    for (int m = 1; m < L; m <<= 1) ss += __shfl_xor(ss, m, L);
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
+    const f32x8 w = to_f32<T>(load16(static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float y = x[i] * r;
+      n[i] = p.norm == DAN_FRONT_NORM_RMS ? rnd<T>(w[i] * rnd<T>(y)) : rnd<T>(y * (1.0f + w[i]));
+    }
+  }
+
+  f32x8 o = n;
+  if (8 * j < p.R) {
+    const int half = p.R / 16;  // lanes per rotary half
+    const int partner = j < half ? j + half : j - half;
+    const u32x4 np = from_f32<T>(n);  // exact: n is already rounded to T
+    u32x4 pp;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t word = np[c];
+      pp[c] = (uint32_t)__shfl((int)word, partner, L);  // lane `partner` of this vector's L lanes
+    }
+    const f32x8 pv = to_f32<T>(pp);
+    const f32x8 cs = to_f32<T>(load16(static_cast<const T *>(p.cos) + t * p.cs_st + 8 * j));
+    const f32x8 sn = to_f32<T>(load16(static_cast<const T *>(p.sin) + t * p.cs_st + 8 * j));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float rot = j < half ? -pv[i] : pv[i];
+      o[i] = rnd<T>(rnd<T>(n[i] * cs[i]) + rnd<T>(rot * sn[i]));
+    }
+  }
+  const u32x4 out = from_f32<T>(o);
+  T *dst = isq ? static_cast<T *>(p.qo) + t * p.qo_st + head * p.qo_sh
+               : static_cast<T *>(p.ko) + t * p.ko_st + head * p.ko_sh;
+  store16(dst + 8 * j, out);
+
+  // Prefix save: the kv-head vector of a saved token also writes its k row
+  // and copies its v row.
+  if (!isq && p.save_of) {
+    const int si = p.save_of[t];
+    if (si >= 0) {
+      const DanFrontSave sv = p.saves[si];
+      const int64_t row = (int64_t)head * sv.len + (t - sv.start);
+      store16(static_cast<T *>(sv.k_dst) + row * D + 8 * j, out);
+      const T *vs = static_cast<const T *>(p.v) + t * p.v_st + head * p.v_sh;
+      store16(static_cast<T *>(sv.v_dst) + row * D + 8 * j, load16(vs + 8 * j));
+    }
+  }
+}
+
+template <typename T, int D>
+hipError_t launch(const Params &p, hipStream_t s) {
+  constexpr int VPB = 256 / (D / 8);
+  const int64_t vectors = (int64_t)p.N * (p.H + p.Hkv);
+  const int64_t grid = (vectors + VPB - 1) / VPB;
+  hipLaunchKernelGGL((qkv_front_kernel<T, D>), dim3((unsigned)grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace dan_front
+
+extern "C" {
+
+int dan_qkv_front_abi_version(void) { return DAN_QKV_FRONT_ABI_VERSION; }
+
+int dan_qkv_front(const DanQkvFrontArgs *a, void *stream) {
+  using namespace dan_front;
+  using dan::fail;
+  dan::g_err[0] = 0;
+  if (!a) return fail(DAN_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != DAN_QKV_FRONT_ABI_VERSION)
+    return fail(DAN_ERR_VERSION, "abi_version %d, library speaks %d", a->abi_version, DAN_QKV_FRONT_ABI_VERSION);
+  const int N = a->num_tokens, H = a->num_heads, Hkv = a->num_kv_heads, D = a->head_dim, R = a->rotary_dim;
+  if (N < 0 || H <= 0 || Hkv <= 0) return fail(DAN_ERR_INVALID_ARGUMENT, "need num_tokens >= 0 and positive head counts");
+  if (D != 64 && D != 128 && D != 256) return fail(DAN_ERR_UNSUPPORTED, "head_dim %d: only 64, 128 and 256 are built", D);
+  if (a->dtype != DAN_DTYPE_BF16 && a->dtype != DAN_DTYPE_F16) return fail(DAN_ERR_UNSUPPORTED, "dtype %d: bf16 or f16", a->dtype);
+  if (R < 0 || R > D || R % 16) return fail(DAN_ERR_INVALID_ARGUMENT, "rotary_dim %d must be a multiple of 16 in [0, %d]", R, D);
+  if (a->norm < DAN_FRONT_NORM_NONE || a->norm > DAN_FRONT_NORM_RMS_ZERO_CENTERED)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "norm %d is not a DanFrontNorm", a->norm);
+  if (a->norm != DAN_FRONT_NORM_NONE && (!a->q_norm_weight || !a->k_norm_weight || !(a->eps >= 0.f)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "a norm needs q_norm_weight, k_norm_weight and eps >= 0");
+  if (a->num_saves < 0 || (a->num_saves > 0 && (!a->save_of || !a->saves || !a->v)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "saves need save_of, saves and v");
+  if (N == 0) return DAN_OK;
+  if (!a->q || !a->k || !a->q_out || !a->k_out || (R > 0 && (!a->cos || !a->sin)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "NULL tensor pointer");
+  if (R > 0 && a->cs_stride_tok < R) return fail(DAN_ERR_INVALID_ARGUMENT, "cs_stride_tok %lld < rotary_dim", (long long)a->cs_stride_tok);
+  // 16-byte accesses: every row start must be 16-byte aligned.
+  const int64_t strides[] = {a->q_stride_tok, a->q_stride_head, a->k_stride_tok, a->k_stride_head, a->qo_stride_tok,
+                             a->qo_stride_head, a->ko_stride_tok, a->ko_stride_head, R > 0 ? a->cs_stride_tok : 0,
+                             a->num_saves > 0 ? a->v_stride_tok : 0, a->num_saves > 0 ? a->v_stride_head : 0};
+  for (int64_t st : strides)
+    if (st % 8) return fail(DAN_ERR_INVALID_ARGUMENT, "strides must be multiples of 8 elements (16-byte rows)");
+  const void *ptrs[] = {a->q, a->k, a->q_out, a->k_out, a->cos, a->sin, a->q_norm_weight, a->k_norm_weight, a->v};
+  for (const void *ptr : ptrs)
+    if (!aligned16(ptr)) return fail(DAN_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+  if ((int64_t)N * (H + Hkv) / (256 / (D / 8)) >= (int64_t)1 << 31) return fail(DAN_ERR_INVALID_ARGUMENT, "too many head vectors");
+
+  Params p;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.cos = a->cos; p.sin = a->sin;
+  p.qw = a->q_norm_weight; p.kw = a->k_norm_weight; p.qo = a->q_out; p.ko = a->k_out;
+  p.q_st = a->q_stride_tok; p.q_sh = a->q_stride_head; p.k_st = a->k_stride_tok; p.k_sh = a->k_stride_head;
+  p.v_st = a->v_stride_tok; p.v_sh = a->v_stride_head; p.cs_st = a->cs_stride_tok;
+  p.qo_st = a->qo_stride_tok; p.qo_sh = a->qo_stride_head; p.ko_st = a->ko_stride_tok; p.ko_sh = a->ko_stride_head;
+  p.save_of = a->num_saves > 0 ? a->save_of : nullptr;
+  p.saves = a->saves;
+  p.N = N; p.H = H; p.Hkv = Hkv; p.R = R; p.norm = a->norm; p.eps = a->eps;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  const bool bf16 = a->dtype == DAN_DTYPE_BF16;
+  if (D == 64) err = bf16 ? launch<__bf16, 64>(p, s) : launch<_Float16, 64>(p, s);
+  else if (D == 128) err = bf16 ? launch<__bf16, 128>(p, s) : launch<_Float16, 128>(p, s);
+  else err = bf16 ? launch<__bf16, 256>(p, s) : launch<_Float16, 256>(p, s);
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "front-end launch failed: %s", hipGetErrorString(err));
+  return DAN_OK;
+}
+
+}  // extern "C"

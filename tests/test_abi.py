@@ -13,6 +13,7 @@ from dan_amd import _native
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dan_tree_attn.h")
+FRONT_HEADER = os.path.join(ROOT, "include", "dan_qkv_front.h")
 
 
 @pytest.fixture(scope="module")
@@ -25,7 +26,7 @@ def lib():
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = open(HEADER).read() + open(FRONT_HEADER).read()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dan_\w+)\s*\(", text, re.M)))
 
 
@@ -45,11 +46,14 @@ STRUCTS = {
     "DanPastDesc": _native.DanPastDesc,
     "DanWorkItem": _native.DanWorkItem,
     "DanTreeAttnArgs": _native.DanTreeAttnArgs,
+    "DanFrontSave": _native.DanFrontSave,
+    "DanQkvFrontArgs": _native.DanQkvFrontArgs,
 }
 
 
 def test_ctypes_layout_matches_header(tmp_path):
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', "int main(void) {"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', '#include "dan_qkv_front.h"',
+             "int main(void) {"]
     for cname, cls in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
@@ -57,6 +61,8 @@ def test_ctypes_layout_matches_header(tmp_path):
     lines.append(f'printf("ABI %d\\n", DAN_TREE_ATTN_ABI_VERSION);')
     lines.append(f'printf("KEY_TILE %d\\n", DAN_TREE_ATTN_KEY_TILE);')
     lines.append('printf("PHASES %d,%d,%d\\n", DAN_TREE_ATTN_PHASES_ALL, DAN_TREE_ATTN_PHASE_PACK, DAN_TREE_ATTN_PHASE_ATTEND);')
+    lines.append('printf("FRONT %d,%d,%d,%d\\n", DAN_QKV_FRONT_ABI_VERSION, DAN_FRONT_NORM_NONE, DAN_FRONT_NORM_RMS, '
+                 'DAN_FRONT_NORM_RMS_ZERO_CENTERED);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -72,6 +78,8 @@ def test_ctypes_layout_matches_header(tmp_path):
     assert int(got["ABI"]) == _native.ABI_VERSION
     assert int(got["KEY_TILE"]) == _native.KEY_TILE
     assert got["PHASES"] == f"{_native.PHASES_ALL},{_native.PHASE_PACK},{_native.PHASE_ATTEND}"
+    assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
+                            f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
 
 
 def test_abi_version_and_tile_q(lib):
@@ -160,3 +168,47 @@ def test_bad_scale_dtype_and_workspace(lib):
         rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**dict(full, **sched))), None)
         assert rc == _native.ERR_INVALID_ARGUMENT
         assert "schedule" in _native.last_error(lib)
+
+
+def _front_args(**kw):
+    a = _native.DanQkvFrontArgs()
+    a.abi_version = _native.FRONT_ABI_VERSION
+    a.dtype = _native.DTYPE_BF16
+    a.num_tokens, a.num_heads, a.num_kv_heads, a.head_dim, a.rotary_dim = 4, 4, 2, 128, 128
+    a.eps = 1e-6
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=7), _native.ERR_VERSION, "abi_version"),
+    (dict(head_dim=96), _native.ERR_UNSUPPORTED, "head_dim"),
+    (dict(dtype=_native.DTYPE_F32), _native.ERR_UNSUPPORTED, "dtype"),
+    (dict(rotary_dim=40), _native.ERR_INVALID_ARGUMENT, "rotary_dim"),
+    (dict(rotary_dim=144), _native.ERR_INVALID_ARGUMENT, "rotary_dim"),
+    (dict(norm=5), _native.ERR_INVALID_ARGUMENT, "norm"),
+    (dict(norm=1), _native.ERR_INVALID_ARGUMENT, "weight"),
+    (dict(num_saves=2), _native.ERR_INVALID_ARGUMENT, "saves"),
+    (dict(num_heads=0), _native.ERR_INVALID_ARGUMENT, "head"),
+])
+def test_front_argument_errors(lib, kw, status, needle):
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(**kw)), None) == status
+    assert needle in _native.last_error(lib)
+
+
+def test_front_checks_pointers_and_alignment(lib):
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(num_tokens=0)), None) == _native.OK  # nothing to do
+    x = (ctypes.c_uint8 * 8192)()
+    p = (ctypes.addressof(x) + 255) // 256 * 256
+    full = dict(q=p, k=p, v=p, cos=p, sin=p, q_out=p, k_out=p, q_stride_tok=512, q_stride_head=128, k_stride_tok=256,
+                k_stride_head=128, qo_stride_tok=512, qo_stride_head=128, ko_stride_tok=256, ko_stride_head=128,
+                cs_stride_tok=128)
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, q=0))), None) == _native.ERR_INVALID_ARGUMENT
+    assert "NULL" in _native.last_error(lib)
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, q=p + 2))), None) == _native.ERR_INVALID_ARGUMENT
+    assert "aligned" in _native.last_error(lib)
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, q_stride_tok=500))), None) == _native.ERR_INVALID_ARGUMENT
+    assert "multiples of 8" in _native.last_error(lib)
+    assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, cs_stride_tok=64))), None) == _native.ERR_INVALID_ARGUMENT
+    assert "cs_stride_tok" in _native.last_error(lib)

@@ -1,0 +1,168 @@
+"""Parity of the gfx950 front end (dan_amd.front.qkv_front -> C ABI) with the
+CPU oracle (oracle/front.py) on identical seeded inputs.
+
+Bars: without a norm the chain is elementwise with the same op order and
+rounding as the eager torch ops, so the outputs must be bit-identical. With a
+norm, the only difference is the summation order of sum(x^2), which can move
+a normalized value by one rounding step; through the rotation that is at
+most one spacing of the largest value of its head row (where x*cos and
+rot*sin cancel, many spacings of the small result). Outputs must be within
+that of the oracle everywhere and bit-identical for at least 99.9 % of the
+elements. Saved rows are bit-identical to the kernel's own outputs."""
+import sys
+
+import pytest
+import torch
+
+from dan_amd import workloads as W
+from dan_amd.attention import attend, segment
+from dan_amd.front import qkv_front
+from oracle import front as OF
+from oracle import tree_attention as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _tables(n, r, dtype, device, seed=0):
+    pos = torch.arange(n, dtype=torch.float32) + 7 * seed
+    inv = 1.0 / (500000.0 ** (torch.arange(0, r, 2, dtype=torch.float64) / r)).float()
+    ang = pos[:, None] * inv[None, :]
+    ang = torch.cat((ang, ang), dim=-1)
+    return ang.cos().to(dtype).to(device), ang.sin().to(dtype).to(device)
+
+
+def _qkv(n, h, hkv, d, dtype, device, seed=0, gate=False):
+    """A fused projection output [N, (H (x2 with gate) + 2 Hkv) * D] and its views."""
+    g = torch.Generator().manual_seed(seed)
+    qd = h * d * (2 if gate else 1)
+    qkv = torch.randn(n, qd + 2 * hkv * d, generator=g).to(dtype).to(device)
+    qg, kx, vx = qkv.split([qd, hkv * d, hkv * d], dim=-1)
+    q = qg.reshape(n, h, 2 * d)[..., :d] if gate else qg.reshape(n, h, d)
+    return q, kx.reshape(n, hkv, d), vx.reshape(n, hkv, d)
+
+
+def _spacing(x, dtype):
+    """Spacing of `dtype` values at |x| (x may be float64)."""
+    xd = x.double().abs()
+    e = torch.floor(torch.log2(torch.where(xd > 0, xd, torch.ones_like(xd))))
+    mant = 7 if dtype == torch.bfloat16 else 10
+    return torch.pow(2.0, e - mant)
+
+
+def check(out, ref, exact):
+    out, ref = out.cpu(), ref.cpu()
+    same = (out == ref) | (out.isnan() & ref.isnan())
+    frac = same.float().mean().item()
+    diff = (out.double() - ref.double()).abs()
+    worst = (diff / _spacing(ref, ref.dtype)).max().item()
+    row_max = ref.double().abs().amax(-1, keepdim=True)
+    worst_row = (diff / _spacing(row_max, ref.dtype)).max().item()
+    say(f"  bit-identical {frac * 100:.4f} %, worst {worst:.2f} spacings of the value, "
+        f"{worst_row:.2f} of its row's largest value")
+    if exact:
+        assert frac == 1.0
+    else:
+        assert worst_row <= 1.0 and frac >= 0.999
+
+
+def run_case(gpu, n, h, hkv, d, r, norm, dtype=torch.bfloat16, gate=False, seed=0):
+    q, k, v = _qkv(n, h, hkv, d, dtype, gpu, seed, gate)
+    cos, sin = _tables(n, r, dtype, gpu, seed) if r else (None, None)
+    g = torch.Generator().manual_seed(seed + 1)
+    wq = (torch.randn(d, generator=g) * 0.2 + (1.0 if norm == "rms" else 0.0)).to(dtype).to(gpu)
+    wk = (torch.randn(d, generator=g) * 0.2 + (1.0 if norm == "rms" else 0.0)).to(dtype).to(gpu)
+    qo, ko, vo = qkv_front(q, k, v, cos, sin, q_norm_weight=wq, k_norm_weight=wk, eps=1e-6, norm=norm)
+    torch.cuda.synchronize()
+    cpu = lambda t: None if t is None else t.cpu()
+    rq, rk, rv, _ = OF.front(cpu(q), cpu(k), cpu(v), cpu(cos), cpu(sin), cpu(wq), cpu(wk), 1e-6, norm)
+    check(qo, rq, exact=norm is None)
+    check(ko, rk, exact=norm is None)
+    assert vo.data_ptr() == v.data_ptr() and vo.shape == (hkv, n, d)
+    return qo, ko, vo
+
+
+def test_llama_8b_shape_no_norm_bit_exact(gpu):
+    say("front: Llama-3-8B shape, 8192 tokens, full RoPE, no q/k norm")
+    run_case(gpu, 8192, 32, 8, 128, 128, None)
+
+
+def test_qk_rms_norm_shape(gpu):
+    say("front: 32/8 heads, head_dim 128, q/k RMSNorm + full RoPE")
+    run_case(gpu, 8192, 32, 8, 128, 128, "rms")
+
+
+def test_qwen35_zero_centered_partial_rotary_gated_q(gpu):
+    say("front: q/gate interleaved, 16/2 heads, head_dim 256, zero-centered norm, rotary 64")
+    run_case(gpu, 1000, 16, 2, 256, 64, "zero_centered", gate=True, seed=3)
+
+
+@pytest.mark.parametrize("d,r", [(64, 64), (64, 32), (128, 0)])
+def test_other_shapes_fp16(gpu, d, r):
+    say(f"front: fp16, head_dim {d}, rotary {r}")
+    run_case(gpu, 333, 8, 2, d, r, "rms", dtype=torch.float16, seed=d + r)
+    run_case(gpu, 333, 8, 2, d, r, None, dtype=torch.float16, seed=d + r)
+
+
+def test_single_token_and_odd_counts(gpu):
+    say("front: N=1 and vector counts that leave a work group partly empty")
+    run_case(gpu, 1, 3, 1, 128, 128, "rms")
+    run_case(gpu, 5, 7, 7, 64, 64, None)
+
+
+def _segments(gpu, n_trunk, lens, save):
+    ids = [0] * n_trunk + sum(([i + 1] * l for i, l in enumerate(lens)), [])
+    return [segment(0, ids, save=save, device=gpu)], len(ids)
+
+
+def test_prefix_save_in_the_same_pass(gpu):
+    say("front: prefix save of 100 trunk rows, k after norm and rotation, v as is")
+    segs, n = _segments(gpu, 120, [16, 24], save=100)
+    q, k, v = _qkv(n, 8, 2, 128, torch.bfloat16, gpu, seed=5)
+    cos, sin = _tables(n, 128, torch.bfloat16, gpu)
+    w = torch.ones(128, dtype=torch.bfloat16, device=gpu)
+    qo, ko, vo = qkv_front(q, k, v, cos, sin, q_norm_weight=w, k_norm_weight=w, norm="rms", segments=segs, layer=3)
+    torch.cuda.synchronize()
+    ks, vs = segs[0].saved[3]
+    assert ks.shape == (2, 100, 128) and ks.is_contiguous() and vs.is_contiguous()
+    assert torch.equal(ks, ko[:, :100]) and torch.equal(vs, vo[:, :100])
+
+
+def test_front_then_attend_matches_oracle_chain(gpu):
+    """The front end feeding the tree-attention kernel, against the oracle's
+    eager chain feeding the oracle's masked attention."""
+    say("front -> attend: config-2-like segments, q/k RMSNorm")
+    w = W.config2(0, device=gpu)
+    n, h, hkv, d = w.num_tokens, w.q.shape[0], w.k.shape[0], w.q.shape[2]
+    q, k, v = _qkv(n, h, hkv, d, torch.bfloat16, gpu, seed=9)
+    cos, sin = _tables(n, d, torch.bfloat16, gpu)
+    wq = torch.full((d,), 1.1, dtype=torch.bfloat16, device=gpu)
+    wk = torch.full((d,), 0.9, dtype=torch.bfloat16, device=gpu)
+    qo, ko, vo = qkv_front(q, k, v, cos, sin, q_norm_weight=wq, k_norm_weight=wk, norm="rms", segments=w.segments,
+                           layer=0)
+    out = attend(qo, ko, vo, w.segments, 0, save=False)
+    torch.cuda.synchronize()
+    rq, rk, rv, _ = OF.front(q.cpu(), k.cpu(), v.cpu(), cos.cpu(), sin.cpu(), wq.cpu(), wk.cpu(), 1e-6, "rms")
+    ref = O.attend_dense(rq, rk, rv, w.segments, 0)
+    rows = torch.cat([torch.arange(s.start, s.end) for s in w.segments])
+    err = (out.float().cpu()[:, rows] - ref[:, rows]).abs().max().item()
+    say(f"  max-abs {err:.3e}")
+    assert err <= 2e-2
+
+
+def test_errors_are_python_exceptions(gpu):
+    say("front: error paths")
+    q, k, v = _qkv(16, 4, 2, 128, torch.bfloat16, gpu)
+    cos, sin = _tables(16, 128, torch.bfloat16, gpu)
+    with pytest.raises(RuntimeError):
+        qkv_front(q.cpu(), k.cpu(), v.cpu(), cos.cpu(), sin.cpu(), norm=None)
+    with pytest.raises(ValueError):
+        qkv_front(q, k, v, cos, sin, norm="rms")  # no weights
+    with pytest.raises(RuntimeError, match="rotary_dim"):
+        qkv_front(q, k, v, cos[:, :40].contiguous(), sin[:, :40].contiguous(), norm=None)
+    with pytest.raises(ValueError):
+        qkv_front(q.float(), k.float(), v.float(), cos, sin, norm=None)
