@@ -163,6 +163,56 @@ def bench_front(args):
     }), flush=True)
 
 
+def bench_plan(args):
+    """Per-forward tile planning: the host planner (numpy tables, schedule
+    and uploads) against the device planner (O(segments) host part, one
+    upload, one planner launch), each until its tables are on the GPU (a
+    synchronize ends every step). The attention call itself is not timed."""
+    from dan_amd import _native, workloads
+    from dan_amd.attention import _num_cus
+    from dan_amd.plan import TilePlan
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    w = workloads.CONFIGS[args.workload](args.seed, device=dev)
+    h, hkv = w.q.shape[0], w.k.shape[0]
+    tile_q, groups, cus = _native.tile_q(h, hkv, lib), _native.head_groups(h, hkv, lib), _num_cus(dev)
+
+    def host():
+        TilePlan.build(w.segments, w.num_tokens, tile_q, dev).schedule(groups, cus)
+
+    def device():
+        TilePlan.build_device(w.segments, w.num_tokens, tile_q, dev, groups, cus)
+
+    res = {}
+    for name, fn in (("host", host), ("device", device)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        wall, gpu = [], []
+        for _ in range(args.steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t = time.perf_counter()
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            wall.append(time.perf_counter() - t)
+            gpu.append(e0.elapsed_time(e1))
+        res[name] = (statistics.median(wall) * 1e6, statistics.median(gpu) * 1e3)
+    print(json.dumps({
+        "metric": "tile planning latency per forward (tables on the GPU), 1 GPU", "value": round(res["device"][0], 1),
+        "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(res["device"][0] / 1e3, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+        "config": {"workload": f"planner-{args.workload}: {len(w.segments)} segments, {w.num_tokens} tokens, "
+                               f"tile_q {tile_q}, {groups} head groups, {cus} CUs", "seed": args.seed},
+        "host_planner_us": round(res["host"][0], 1), "device_planner_us": round(res["device"][0], 1),
+        "device_stream_us": round(res["device"][1], 1), "speedup": round(res["host"][0] / res["device"][0], 2),
+        "roofline": None, "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -177,6 +227,8 @@ def main():
     ap.add_argument("--front", action="store_true",
                     help="measure the attention front end (q/k norm + RoPE + layout) on --workload c3 or c4 "
                          "instead of the attention")
+    ap.add_argument("--plan", action="store_true",
+                    help="measure per-forward tile planning (host planner against the device planner) on --workload")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, run --steps plain device copies of this many MiB (the calibration "
                          "kernel for the HBM byte counters)")
@@ -191,6 +243,9 @@ def main():
 
     if args.copy_mib:
         copy_calibration(args.copy_mib, args.steps)
+        return
+    if args.plan:
+        bench_plan(args)
         return
     if args.front:
         if args.workload not in FRONT_SHAPES:

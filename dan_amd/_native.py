@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in include/dan_tree_attn.h.
+"""ctypes binding of the C ABI in include/dan_tree_attn.h (with
+include/dan_qkv_front.h and include/dan_tree_plan.h).
 
 The shared library is plain C ABI (no torch types), built in-tree by
 ``dan_amd._build`` into ``dan_amd/_lib/``. It must be loaded after torch has
@@ -93,8 +94,21 @@ class DanQkvFrontArgs(ctypes.Structure):
                 ("save_of", _vp), ("saves", _vp), ("num_saves", _i32)]
 
 
+PLAN_ABI_VERSION = 1
+PLAN_MAX_WORK, PLAN_MAX_SLOTS, PLAN_MAX_SEGMENTS, PLAN_MAX_BRANCHES = 4096, 256, 1024, 4096
+
+
+class DanTreePlanArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("num_tokens", _i32), ("num_segments", _i32), ("num_branches", _i32),
+                ("num_work", _i32), ("num_cols", _i32), ("tile_q", _i32), ("groups", _i32), ("num_cus", _i32),
+                ("overhead", _i32),
+                ("segments", _vp), ("branch_starts", _vp),
+                ("key_lo", _vp), ("col_seg", _vp), ("work", _vp), ("cost", _vp), ("units", _vp), ("sched_off", _vp)]
+
+
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
-           "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version")
+           "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
+           "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -128,10 +142,16 @@ def load(path=LIB_PATH):
         lib.dan_qkv_front.restype = ctypes.c_int
         lib.dan_qkv_front_abi_version.argtypes = []
         lib.dan_qkv_front_abi_version.restype = ctypes.c_int
-        got = lib.dan_tree_attn_abi_version()
-        if got != ABI_VERSION or lib.dan_qkv_front_abi_version() != FRONT_ABI_VERSION:
-            raise RuntimeError(f"{path} speaks ABI {got} / front end {lib.dan_qkv_front_abi_version()}, this package "
-                               f"{ABI_VERSION} / {FRONT_ABI_VERSION}; rebuild it")
+        lib.dan_tree_attn_plan.argtypes = [ctypes.POINTER(DanTreePlanArgs), _vp]
+        lib.dan_tree_attn_plan.restype = ctypes.c_int
+        lib.dan_tree_attn_plan_slots.argtypes = [_i32, _i32, _i32]
+        lib.dan_tree_attn_plan_slots.restype = ctypes.c_int
+        lib.dan_tree_attn_plan_abi_version.argtypes = []
+        lib.dan_tree_attn_plan_abi_version.restype = ctypes.c_int
+        got = (lib.dan_tree_attn_abi_version(), lib.dan_qkv_front_abi_version(), lib.dan_tree_attn_plan_abi_version())
+        if got != (ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION):
+            raise RuntimeError(f"{path} speaks ABI versions {got} (attention, front end, planner), this package "
+                               f"{(ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION)}; rebuild it")
         if path == LIB_PATH:
             _lib = lib
         return lib
@@ -171,3 +191,16 @@ def front(args, stream, lib=None):
     rc = lib.dan_qkv_front(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_qkv_front failed ({rc}): {last_error(lib)}")
+
+
+def plan_slots(num_work, groups, num_cus, lib=None):
+    """Slots of the device planner's schedule (0: invalid arguments)."""
+    return (lib or load()).dan_tree_attn_plan_slots(num_work, groups, num_cus)
+
+
+def plan(args, stream, lib=None):
+    """Launch the device-side tile planner; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_tree_attn_plan(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_tree_attn_plan failed ({rc}): {last_error(lib)}")

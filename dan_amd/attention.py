@@ -194,11 +194,33 @@ def _kernel_view(t):
     return t if _aligned(t) and small else t.contiguous()
 
 
-def get_plan(segments, num_tokens, tile_q, device):
-    """The cached tile plan of this batch (built on first use)."""
+# Which tile planner builds a batch's tables: "device" (one upload and one
+# planner launch per forward; batches beyond its limits go to the host
+# planner) or "host" (numpy). Both make the same tables.
+PLANNER = "device"
+
+
+def get_plan(segments, num_tokens, tile_q, device, groups=None, num_cus=None, planner=None):
+    """The cached tile plan of this batch (built on first use). With
+    ``groups`` and ``num_cus`` the device planner also makes the schedule."""
+    planner = planner or PLANNER
+    if planner not in ("device", "host"):
+        raise ValueError(f"planner {planner!r}: 'device' or 'host'")
     plan = getattr(segments, "tile_plan", None)
-    if plan is None or not plan.matches(num_tokens, tile_q, device):
-        plan = TilePlan.build(segments, num_tokens, tile_q, device)
+    want_device = planner == "device" and groups is not None and torch.device(device).type == "cuda"
+    stale = plan is None or not plan.matches(num_tokens, tile_q, device)
+    if not stale and want_device and plan.cost is None and (groups, num_cus) not in plan.schedules:
+        stale = True  # device-built for another head layout
+    if stale:
+        plan = None
+        if want_device:
+            try:
+                plan = TilePlan.build_device(segments, num_tokens, tile_q, device, groups, num_cus)
+            except ValueError as e:
+                if "limits" not in str(e):
+                    raise
+        if plan is None:
+            plan = TilePlan.build(segments, num_tokens, tile_q, device)
         if isinstance(segments, Batch):
             segments.tile_plan = plan
     return plan
@@ -283,7 +305,8 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     tile_q = _native.tile_q(h, hkv, lib)
     if tile_q <= 0:
         raise ValueError(f"unsupported head layout H={h}, Hkv={hkv}")
-    plan = get_plan(segments, n, tile_q, q.device)
+    groups = _native.head_groups(h, hkv, lib)
+    plan = get_plan(segments, n, tile_q, q.device, groups=groups, num_cus=_num_cus(q.device))
     table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
     out_dtype = torch.bfloat16 if q.dtype == E4M3 else q.dtype
     if q.dtype == E4M3:
@@ -291,7 +314,7 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     qk_dtype = _qk_dtype(q.dtype)
     q, k, v = _kernel_view(q.to(qk_dtype)), _kernel_view(k.to(qk_dtype)), _kernel_view(v)
     out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
-    if len(plan.work):
+    if plan.num_work:
         nbytes = _native.workspace_size(hkv, d, plan.vt_cols, lib)
         ws = _workspace(plan, nbytes, q.device)
         a = _native.DanTreeAttnArgs()
@@ -307,7 +330,7 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
         a.out, a.o_stride_tok, a.o_stride_head = out.data_ptr(), out.stride(0), out.stride(1)
         a.segments, a.num_segments = plan.segs_d.data_ptr(), len(plan.segs)
         a.pasts, a.num_pasts = table.data_ptr(), len(plan.past_dicts)
-        a.work, a.num_work = plan.work_d.data_ptr(), len(plan.work)
+        a.work, a.num_work = plan.work_d.data_ptr(), plan.num_work
         a.key_lo = plan.key_lo_d.data_ptr()
         a.tile_q = tile_q
         a.vt_cols = plan.vt_cols
@@ -316,7 +339,6 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
         if q.dtype == E4M3:
             a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
         a.phases = phases
-        groups = _native.head_groups(h, hkv, lib)
         units, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
         a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
         _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)

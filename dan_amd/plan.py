@@ -25,6 +25,13 @@ calls. Here the same segment metadata becomes:
 It is built once per forward and cached on the ``Batch`` (as
 dan/attention.py:211-215 caches ``layout``); only the per-layer table of
 prefix-cache pointers is rebuilt per layer.
+
+Two builders make the same tables. ``TilePlan.build`` runs here on the host
+(numpy). ``TilePlan.build_device`` keeps O(segments) work on the host
+(``device_inputs``: each segment's first V^T column, first work item and
+first branch) and makes one upload and one launch of the device planner
+(include/dan_tree_plan.h), which builds key_lo, col_seg, the work list and the
+schedule on the GPU, on the current stream.
 """
 from dataclasses import dataclass, field
 
@@ -106,6 +113,33 @@ def build_tables(segments, num_tokens, tile_q, key_tile=KEY_TILE):
     cost = (work[:, 3].astype(np.int64) + work[:, 5] - work[:, 4]) if len(work) else np.zeros(0, np.int64)
     order = np.argsort(-cost, kind="stable")
     return segs, work[order], key_lo, cost[order], past_dicts, np.array(col_seg, np.int32)
+
+
+def device_inputs(segments, num_tokens, tile_q, key_tile=KEY_TILE):
+    """The host part of the device planner: (segs int32 [S, 8], branch_starts
+    int32 [B], num_work, num_cols, past_dicts). segs rows are DanSegmentDesc
+    with reserved[0] = the segment's first work item and reserved[1] its
+    first branch; the counts are sums of ceil(n / tile_q) and
+    ceil((P + n) / key_tile)."""
+    if tile_q <= 0:
+        raise ValueError(f"tile_q {tile_q}: unsupported head layout")
+    validate_segments(segments, num_tokens)
+    segs = np.zeros((len(segments), 8), np.int32)
+    past_dicts, past_index, starts = [], {}, []
+    w = c = 0
+    for i, s in enumerate(segments):
+        n = s.end - s.start
+        p = s.past_len if s.past else 0
+        pidx = -1
+        if s.past:
+            pidx = past_index.setdefault(id(s.past), len(past_dicts))
+            if pidx == len(past_dicts):
+                past_dicts.append(s.past)
+        segs[i] = (s.start, n, s.trunk, p, pidx, c * key_tile, w, len(starts))
+        starts += [a for a, _ in s.branches]
+        w += _ceil_div(n, tile_q)
+        c += _ceil_div(p + n, key_tile)
+    return segs, np.array(starts, np.int32), w, c, past_dicts
 
 
 def schedule(cost, groups, num_cus, overhead=1):
@@ -200,11 +234,14 @@ class TilePlan:
     num_tokens: int
     device: object
     segs: np.ndarray
-    work: np.ndarray
-    key_lo: np.ndarray
-    cost: np.ndarray
+    work: np.ndarray  # host-built only (None from the device planner)
+    key_lo: np.ndarray  # host-built only
+    cost: np.ndarray  # host-built only
     past_dicts: list
-    col_seg: np.ndarray = None
+    col_seg: np.ndarray = None  # host-built only
+    num_work: int = 0
+    num_cols: int = 0
+    cost_d: object = None  # device planner: key tiles per item, longest first
     segs_d: object = None
     work_d: object = None
     key_lo_d: object = None
@@ -218,16 +255,58 @@ class TilePlan:
         import torch
 
         segs, work, key_lo, cost, past_dicts, col_seg = build_tables(segments, num_tokens, tile_q)
-        plan = cls(tile_q, num_tokens, torch.device(device), segs, work, key_lo, cost, past_dicts, col_seg)
+        plan = cls(tile_q, num_tokens, torch.device(device), segs, work, key_lo, cost, past_dicts, col_seg,
+                   num_work=len(work), num_cols=len(col_seg))
         plan.segs_d = _upload(segs, device)
         plan.work_d = _upload(work, device)
         plan.key_lo_d = _upload(key_lo, device)
         plan.col_seg_d = _upload(col_seg, device)
         return plan
 
+    @classmethod
+    def build_device(cls, segments, num_tokens, tile_q, device, groups, num_cus, overhead=1):
+        """The same tables from the device planner (one upload, one launch on
+        the current stream); the schedule is made for ``groups`` head groups
+        on ``num_cus`` compute units. Raises ValueError when the batch exceeds
+        the planner's limits (see ``device_fits``)."""
+        import torch
+
+        from . import _native
+
+        segs, starts, w, c, past_dicts = device_inputs(segments, num_tokens, tile_q)
+        lib = _native.load()
+        slots = _native.plan_slots(w, groups, num_cus, lib) if w else 0
+        if (w > _native.PLAN_MAX_WORK or (w and slots // groups > _native.PLAN_MAX_SLOTS)
+                or len(segs) > _native.PLAN_MAX_SEGMENTS or len(starts) > _native.PLAN_MAX_BRANCHES):
+            raise ValueError(f"{w} work items, {slots} slots, {len(segs)} segments or {len(starts)} branches "
+                             "exceed the device planner's limits")
+        dev = torch.device(device)
+        plan = cls(tile_q, num_tokens, dev, segs, None, None, None, past_dicts, None, num_work=w, num_cols=c)
+        blob = _upload(np.concatenate([segs.ravel(), starts]).astype(np.int32), dev)  # the one upload
+        plan.segs_d = blob[:segs.size]
+        plan.key_lo_d = torch.empty(num_tokens, dtype=torch.int32, device=dev)
+        plan.col_seg_d = torch.empty(max(c, 1), dtype=torch.int32, device=dev)
+        plan.work_d = torch.empty((max(w, 1), 8), dtype=torch.int32, device=dev)
+        plan.cost_d = torch.empty(max(w, 1), dtype=torch.int32, device=dev)
+        units = torch.empty((max(w * groups, 1), 16), dtype=torch.int32, device=dev)
+        off = torch.empty(slots + 1, dtype=torch.int32, device=dev)
+        if w:
+            a = _native.DanTreePlanArgs()
+            a.abi_version = _native.PLAN_ABI_VERSION
+            a.num_tokens, a.num_segments, a.num_branches = num_tokens, len(segs), len(starts)
+            a.num_work, a.num_cols, a.tile_q, a.groups, a.num_cus, a.overhead = w, c, tile_q, groups, num_cus, overhead
+            a.segments = blob.data_ptr()
+            a.branch_starts = blob.data_ptr() + 4 * segs.size
+            a.key_lo, a.col_seg, a.work, a.cost = (plan.key_lo_d.data_ptr(), plan.col_seg_d.data_ptr(),
+                                                   plan.work_d.data_ptr(), plan.cost_d.data_ptr())
+            a.units, a.sched_off = units.data_ptr(), off.data_ptr()
+            _native.plan(a, torch.cuda.current_stream(dev).cuda_stream, lib)
+        plan.schedules[(groups, num_cus)] = (units, off, slots)
+        return plan
+
     @property
     def vt_cols(self):
-        return int(len(self.col_seg) * KEY_TILE)
+        return int(self.num_cols * KEY_TILE)
 
     def matches(self, num_tokens, tile_q, device):
         import torch
@@ -236,9 +315,12 @@ class TilePlan:
 
     def schedule(self, groups, num_cus):
         """Device copies of the unit records of ``schedule(self.cost, groups,
-        num_cus)`` and of its slot offsets, and the slot count (cached)."""
+        num_cus)`` and of its slot offsets, and the slot count (cached; a plan
+        from the device planner carries the schedule it was built for)."""
         key = (groups, num_cus)
         if key not in self.schedules:
+            if self.cost is None:
+                raise ValueError(f"this plan was scheduled on the device for {list(self.schedules)}, not {key}")
             sched, off = schedule(self.cost, groups, num_cus)
             units = unit_records(self.segs, self.work, sched, groups)
             self.schedules[key] = (_upload(units, self.device), _upload(off, self.device), len(off) - 1)
@@ -246,7 +328,7 @@ class TilePlan:
 
     def key_tiles(self):
         """Total key tiles the work list visits (per kv head and head chunk)."""
-        return int(self.cost.sum())
+        return int(self.cost.sum() if self.cost is not None else self.cost_d[:self.num_work].sum().item())
 
 
 def _upload(arr, device):

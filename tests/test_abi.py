@@ -1,5 +1,5 @@
 """The C ABI without a GPU: the built library loads and exports every function
-include/dan_tree_attn.h declares, the ctypes mirror has the header's exact
+include/dan_tree_attn.h, dan_qkv_front.h and dan_tree_plan.h declare, the ctypes mirror has the header's exact
 struct layout (checked by compiling the header with gcc), and argument
 errors come back as status codes with messages before any GPU call."""
 import ctypes
@@ -14,6 +14,7 @@ from dan_amd import _native
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dan_tree_attn.h")
 FRONT_HEADER = os.path.join(ROOT, "include", "dan_qkv_front.h")
+PLAN_HEADER = os.path.join(ROOT, "include", "dan_tree_plan.h")
 
 
 @pytest.fixture(scope="module")
@@ -26,7 +27,7 @@ def lib():
 
 
 def declared_functions():
-    text = open(HEADER).read() + open(FRONT_HEADER).read()
+    text = open(HEADER).read() + open(FRONT_HEADER).read() + open(PLAN_HEADER).read()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dan_\w+)\s*\(", text, re.M)))
 
 
@@ -48,12 +49,13 @@ STRUCTS = {
     "DanTreeAttnArgs": _native.DanTreeAttnArgs,
     "DanFrontSave": _native.DanFrontSave,
     "DanQkvFrontArgs": _native.DanQkvFrontArgs,
+    "DanTreePlanArgs": _native.DanTreePlanArgs,
 }
 
 
 def test_ctypes_layout_matches_header(tmp_path):
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', '#include "dan_qkv_front.h"',
-             "int main(void) {"]
+             '#include "dan_tree_plan.h"', "int main(void) {"]
     for cname, cls in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
@@ -63,6 +65,8 @@ def test_ctypes_layout_matches_header(tmp_path):
     lines.append('printf("PHASES %d,%d,%d\\n", DAN_TREE_ATTN_PHASES_ALL, DAN_TREE_ATTN_PHASE_PACK, DAN_TREE_ATTN_PHASE_ATTEND);')
     lines.append('printf("FRONT %d,%d,%d,%d\\n", DAN_QKV_FRONT_ABI_VERSION, DAN_FRONT_NORM_NONE, DAN_FRONT_NORM_RMS, '
                  'DAN_FRONT_NORM_RMS_ZERO_CENTERED);')
+    lines.append('printf("PLAN %d,%d,%d,%d,%d\\n", DAN_TREE_PLAN_ABI_VERSION, DAN_TREE_PLAN_MAX_WORK, '
+                 'DAN_TREE_PLAN_MAX_SLOTS, DAN_TREE_PLAN_MAX_SEGMENTS, DAN_TREE_PLAN_MAX_BRANCHES);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -80,6 +84,8 @@ def test_ctypes_layout_matches_header(tmp_path):
     assert got["PHASES"] == f"{_native.PHASES_ALL},{_native.PHASE_PACK},{_native.PHASE_ATTEND}"
     assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
                             f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
+    assert got["PLAN"] == (f"{_native.PLAN_ABI_VERSION},{_native.PLAN_MAX_WORK},{_native.PLAN_MAX_SLOTS},"
+                           f"{_native.PLAN_MAX_SEGMENTS},{_native.PLAN_MAX_BRANCHES}")
 
 
 def test_abi_version_and_tile_q(lib):
@@ -212,3 +218,52 @@ def test_front_checks_pointers_and_alignment(lib):
     assert "multiples of 8" in _native.last_error(lib)
     assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, cs_stride_tok=64))), None) == _native.ERR_INVALID_ARGUMENT
     assert "cs_stride_tok" in _native.last_error(lib)
+
+
+def test_plan_slots(lib):
+    """k = max(1, min(num_cus // groups, num_work)) slots per head group, as
+    dan_amd.plan.schedule makes them."""
+    assert _native.plan_slots(130, 8, 256, lib) == 256
+    assert _native.plan_slots(6, 8, 256, lib) == 48
+    assert _native.plan_slots(5, 300, 256, lib) == 300
+    assert _native.plan_slots(0, 8, 256, lib) == 0
+    assert lib.dan_tree_attn_plan_abi_version() == _native.PLAN_ABI_VERSION
+
+
+def _plan_args(**kw):
+    a = _native.DanTreePlanArgs()
+    a.abi_version = _native.PLAN_ABI_VERSION
+    a.num_tokens, a.num_segments, a.num_branches, a.num_work, a.num_cols = 64, 1, 0, 1, 1
+    a.tile_q, a.groups, a.num_cus, a.overhead = 64, 8, 256, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=7), _native.ERR_VERSION, "abi_version"),
+    (dict(num_work=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+    (dict(num_segments=0), _native.ERR_INVALID_ARGUMENT, "segments"),
+    (dict(tile_q=0), _native.ERR_INVALID_ARGUMENT, "positive"),
+    (dict(num_work=_native.PLAN_MAX_WORK + 1), _native.ERR_UNSUPPORTED, "num_work"),
+    (dict(num_segments=_native.PLAN_MAX_SEGMENTS + 1), _native.ERR_UNSUPPORTED, "segments"),
+    (dict(num_branches=_native.PLAN_MAX_BRANCHES + 1), _native.ERR_UNSUPPORTED, "branches"),
+    (dict(groups=1, num_cus=1024), _native.ERR_INVALID_ARGUMENT, "NULL"),  # one slot (W = 1) but no tables
+    (dict(), _native.ERR_INVALID_ARGUMENT, "NULL"),
+])
+def test_plan_argument_errors(lib, kw, status, needle):
+    rc = lib.dan_tree_attn_plan(ctypes.byref(_plan_args(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_plan_too_many_slots(lib):
+    a = _plan_args(num_work=1000, groups=1, num_cus=1024)
+    assert lib.dan_tree_attn_plan(ctypes.byref(a), None) == _native.ERR_UNSUPPORTED
+    assert "slots" in _native.last_error(lib)
+
+
+def test_plan_empty_and_null(lib):
+    assert lib.dan_tree_attn_plan(None, None) == _native.ERR_INVALID_ARGUMENT
+    assert lib.dan_tree_attn_plan(ctypes.byref(_plan_args(num_work=0)), None) == _native.OK
+    assert _native.last_error(lib) == ""

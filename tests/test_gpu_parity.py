@@ -356,9 +356,11 @@ def test_schedule_order_is_invisible(gpu):
     from dan_amd.attention import _num_cus, get_plan
     w = W.config3(0, device=gpu)
     say("schedule variants c3")
-    ref = attend(w.q, w.k, w.v, w.segments, 0).clone()
     h, hkv = w.q.shape[0], w.k.shape[0]
-    plan = get_plan(w.segments, w.num_tokens, _native.tile_q(h, hkv), w.q.device)
+    plan = plan_mod.TilePlan.build(w.segments, w.num_tokens, _native.tile_q(h, hkv), w.q.device)  # host tables
+    w.segments.tile_plan = plan
+    ref = attend(w.q, w.k, w.v, w.segments, 0).clone()
+    assert get_plan(w.segments, w.num_tokens, _native.tile_q(h, hkv), w.q.device) is plan
     groups = _native.head_groups(h, hkv)
     key = (groups, _num_cus(w.q.device))
     planned = plan.schedules[key]

@@ -10,7 +10,7 @@ from hypothesis import strategies as st
 
 from dan_amd import workloads as W
 from dan_amd.attention import Batch, Segment, segment
-from dan_amd.plan import KEY_TILE, build_tables, schedule, unit_records, validate_segments
+from dan_amd.plan import KEY_TILE, build_tables, device_inputs, schedule, unit_records, validate_segments
 from oracle import tree_attention as O
 
 
@@ -185,3 +185,35 @@ def test_schedule_fewer_items_than_cus():
     sched, off, loads, _ = check_schedule(cost, 8, 256)
     assert len(off) - 1 == 24 and (np.diff(off) == 1).all()  # one unit per work group
     assert len(schedule(np.zeros(0, np.int64), 8, 256)[0]) == 0
+
+
+@settings(max_examples=40, deadline=None)
+@given(st.integers(0, 2 ** 31 - 1), st.sampled_from([64, 128, 256]))
+def test_device_planner_inputs(seed, tile_q):
+    """The host part of the device planner: the segment table equals the host
+    planner's, reserved[0] / reserved[1] are each segment's first work item
+    and first branch, and the counts are the host planner's list lengths."""
+    rng = np.random.default_rng(seed)
+    structure, pasts = [], []
+    for _ in range(int(rng.integers(1, 6))):
+        trunk = int(rng.integers(0, 300))
+        lens = [int(x) for x in rng.integers(1, 100, int(rng.integers(0, 6)))]
+        if trunk + sum(lens) == 0:
+            trunk = 1
+        structure.append((trunk, lens))
+        pasts.append(int(rng.integers(1, 200)) if rng.random() < 0.5 else 0)
+    w = W.build("random", structure, 2, 1, 64, torch.float32, "cpu", rng, per_segment_past=pasts)
+    segs, starts, nw, nc, past_dicts = device_inputs(w.segments, w.num_tokens, tile_q)
+    hsegs, work, key_lo, cost, hpast, col_seg = build_tables(w.segments, w.num_tokens, tile_q)
+    assert (segs[:, :6] == hsegs[:, :6]).all()
+    assert nw == len(work) and nc == len(col_seg) and len(past_dicts) == len(hpast)
+    item_of = np.bincount(work[:, 0], minlength=len(segs))  # items per segment
+    assert (segs[:, 6] == np.concatenate([[0], np.cumsum(item_of)[:-1]])).all()
+    at = 0
+    for i, s in enumerate(w.segments):
+        assert segs[i, 7] == at
+        for a, b in s.branches:
+            assert starts[at] == a
+            assert (key_lo[a:b] == (s.past_len if s.past else 0) + a - s.start).all()
+            at += 1
+    assert at == len(starts)
