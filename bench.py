@@ -163,6 +163,105 @@ def bench_front(args):
     }), flush=True)
 
 
+LLAMA8B_LINEARS = (("qkv_proj", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up_proj", 28672, 4096),
+                   ("down_proj", 4096, 14336))  # (name, out_features, in_features) of one decoder layer
+
+
+def _event_ms(fn, steps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in ev)
+
+
+def bench_fp8_linear(args):
+    """One decoder layer's FP8 linears (dan_amd.quant.FP8Linear, rowwise) at
+    Llama-3-8B shapes on 8192 tokens: activation quantization (this
+    package's kernel) + hipBLASLt's fp8 GEMM per linear. One step = the four
+    linears' forwards on synthetic bf16 activations and random weights."""
+    from torch import nn
+
+    from dan_amd.quant import FP8Linear, fp8_quantize
+
+    dev = torch.device("cuda:0")
+    m = 8192
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    layers, xs = [], []
+    for name, n, k in LLAMA8B_LINEARS:
+        lin = nn.Linear(k, n, bias=False, device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(n, k, device=dev, generator=g) * 0.02)
+        layers.append(FP8Linear(lin, rowwise=True))
+        xs.append(torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16))
+    flops = sum(2 * m * n * k for _, n, k in LLAMA8B_LINEARS)
+
+    def step():
+        for f, x in zip(layers, xs):
+            f(x)
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        step()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t) / args.steps
+    # parts, timed per launch on the stream
+    quant_ms = [_event_ms(lambda x=x: fp8_quantize(x), args.steps) for x in xs]
+    qs = [fp8_quantize(x) for x in xs]
+    gemm_ms = [_event_ms(lambda f=f, q=q: torch._scaled_mm(q[0], f.weight.t(), scale_a=q[1], scale_b=f.weight_scale,
+                                                           out_dtype=torch.bfloat16), args.steps)
+               for f, q in zip(layers, qs)]
+
+    def eager_quant(x):  # dan/fused.py:85-91 as eager torch ops on this GPU
+        xf = x.float()
+        scale = xf.abs().amax(dim=-1, keepdim=True).clamp(min=1e-12) / 448.0
+        return (xf / scale).to(torch.float8_e4m3fn), scale
+
+    eager_ms = [_event_ms(lambda x=x: eager_quant(x), args.steps) for x in xs]
+    qbytes = [m * k * 2 + m * k + m * 4 for _, _, k in LLAMA8B_LINEARS]
+    gemm_tf = flops / (sum(gemm_ms) * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import quant as OQ
+        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        rows = 64
+        sample_flops = sum(2 * rows * n * k for _, n, k in LLAMA8B_LINEARS)
+        cx = [torch.randn(rows, k).to(torch.bfloat16) for _, _, k in LLAMA8B_LINEARS]
+        cw = [(f.weight.cpu(), f.weight_scale.cpu()) for f in layers]
+        tc = time.perf_counter()
+        for x, (wq, ws) in zip(cx, cw):
+            xq, sx = OQ.fp8_quantize(x, True)
+            OQ.fp8_linear(xq, sx, wq, ws)
+        tc = time.perf_counter() - tc
+        cpu = {"value": round(sample_flops / tc / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"{rows} tokens through the four linears with the oracle (fp32 quantize, "
+                                         f"float64 GEMM): {tc:.2f} s; CPU: {cpu_model()}"}
+    print(json.dumps({
+        "metric": "FP8 decoder linears (Llama-3-8B layer, 8192 tokens) TFLOP/s, 1 GPU",
+        "value": round(flops / wall / 1e12, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8", "data": "synthetic",
+        "config": {"workload": "fp8-linears: Llama-3-8B qkv/o/gate_up/down at 8192 tokens, rowwise e4m3",
+                   "seed": args.seed},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
+                     "frac": round(gemm_tf / PEAK_TFLOPS["fp8"], 4), "traffic": None,
+                     "gemm_ms": [round(x, 4) for x in gemm_ms], "quant_ms": [round(x, 4) for x in quant_ms],
+                     "quant_gbps": [round(b / (t * 1e-3) / 1e9, 1) for b, t in zip(qbytes, quant_ms)],
+                     "quant_hbm_frac": round(sum(qbytes) / (sum(quant_ms) * 1e-3) / 1e9 / HBM_GBPS, 4),
+                     "eager_quant_ms": [round(x, 4) for x in eager_ms]},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def bench_plan(args):
     """Per-forward tile planning: the host planner (numpy tables, schedule
     and uploads) against the device planner (O(segments) host part, one
@@ -227,6 +326,8 @@ def main():
     ap.add_argument("--front", action="store_true",
                     help="measure the attention front end (q/k norm + RoPE + layout) on --workload c3 or c4 "
                          "instead of the attention")
+    ap.add_argument("--fp8-linear", action="store_true",
+                    help="measure one Llama-3-8B decoder layer's FP8 linears (quantize + hipBLASLt GEMM) at 8192 tokens")
     ap.add_argument("--plan", action="store_true",
                     help="measure per-forward tile planning (host planner against the device planner) on --workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -246,6 +347,9 @@ def main():
         return
     if args.plan:
         bench_plan(args)
+        return
+    if args.fp8_linear:
+        bench_fp8_linear(args)
         return
     if args.front:
         if args.workload not in FRONT_SHAPES:

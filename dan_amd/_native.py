@@ -1,5 +1,5 @@
 """ctypes binding of the C ABI in include/dan_tree_attn.h (with
-include/dan_qkv_front.h and include/dan_tree_plan.h).
+include/dan_qkv_front.h, include/dan_tree_plan.h and include/dan_fp8.h).
 
 The shared library is plain C ABI (no torch types), built in-tree by
 ``dan_amd._build`` into ``dan_amd/_lib/``. It must be loaded after torch has
@@ -106,9 +106,19 @@ class DanTreePlanArgs(ctypes.Structure):
                 ("key_lo", _vp), ("col_seg", _vp), ("work", _vp), ("cost", _vp), ("units", _vp), ("sched_off", _vp)]
 
 
+FP8_ABI_VERSION = 1
+FP8_SCALE_TENSOR, FP8_SCALE_ROW = 0, 1
+
+
+class DanFp8QuantArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("dtype", _i32), ("rows", _i32), ("cols", _i32), ("mode", _i32),
+                ("reserved", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
+
+
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
-           "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version")
+           "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
+           "dan_fp8_quantize", "dan_fp8_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -148,10 +158,16 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_plan_slots.restype = ctypes.c_int
         lib.dan_tree_attn_plan_abi_version.argtypes = []
         lib.dan_tree_attn_plan_abi_version.restype = ctypes.c_int
-        got = (lib.dan_tree_attn_abi_version(), lib.dan_qkv_front_abi_version(), lib.dan_tree_attn_plan_abi_version())
-        if got != (ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION):
-            raise RuntimeError(f"{path} speaks ABI versions {got} (attention, front end, planner), this package "
-                               f"{(ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION)}; rebuild it")
+        lib.dan_fp8_quantize.argtypes = [ctypes.POINTER(DanFp8QuantArgs), _vp]
+        lib.dan_fp8_quantize.restype = ctypes.c_int
+        lib.dan_fp8_abi_version.argtypes = []
+        lib.dan_fp8_abi_version.restype = ctypes.c_int
+        got = (lib.dan_tree_attn_abi_version(), lib.dan_qkv_front_abi_version(), lib.dan_tree_attn_plan_abi_version(),
+               lib.dan_fp8_abi_version())
+        want = (ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION, FP8_ABI_VERSION)
+        if got != want:
+            raise RuntimeError(f"{path} speaks ABI versions {got} (attention, front end, planner, fp8), this package "
+                               f"{want}; rebuild it")
         if path == LIB_PATH:
             _lib = lib
         return lib
@@ -204,3 +220,11 @@ def plan(args, stream, lib=None):
     rc = lib.dan_tree_attn_plan(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_tree_attn_plan failed ({rc}): {last_error(lib)}")
+
+
+def fp8_quantize(args, stream, lib=None):
+    """Launch the e4m3 quantizer; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_fp8_quantize(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_fp8_quantize failed ({rc}): {last_error(lib)}")

@@ -1,0 +1,196 @@
+// e4m3 quantizer for dan's FP8 decoder linears on gfx950 (MI355X, CDNA4):
+// dan/fused.py:85-91 (fp8_quantize) as one pass over x per row.
+//
+//   amax  = max |x| over a row (rowwise) or the tensor
+//   scale = max(amax, 1e-12) / 448               fp32, correctly rounded
+//   xq    = e4m3fn(x / scale)                     fp32 divide, then v_cvt_pk_fp8_f32
+//                                                 (gfx950: OCP e4m3, round to
+//                                                 nearest even)
+// |x / scale| <= 448 (up to the divide's rounding, which rounds back to 448),
+// so no code saturates.
+//
+// Rowwise: one work group of 256 threads per row; each thread takes 8
+// consecutive values (one 16-byte load for 16-bit inputs) per 2048 of the
+// row, reduces |x| (wave shuffles, then LDS across the 4 waves), and on a
+// second pass over the row (now in L2) writes 8 codes per 8 values.
+// Per tensor: a zero fill, the same per-row amax folded into one fp32 by a
+// vector atomic max on its bits (non-negative floats order as integers),
+// the scale, then the quantizing pass with the one scale.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dan_fp8.h"
+
+namespace dan {
+int fail(int status, const char *fmt, ...);  // tree_attn.hip: sets the thread's last-error message
+extern thread_local char g_err[512];
+}  // namespace dan
+
+namespace dan_fp8 {
+
+constexpr int kThreads = 256;
+constexpr float kE4m3Max = 448.0f;  // torch.finfo(torch.float8_e4m3fn).max (dan/quant.py:16)
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+#define DAN_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+__device__ inline f32x8 load8(const T *p);
+template <>
+__device__ inline f32x8 load8<__bf16>(const __bf16 *p) {
+  return __builtin_convertvector(__builtin_bit_cast(bf16x8, *(const DAN_GLOBAL u32x4 *)p), f32x8);
+}
+template <>
+__device__ inline f32x8 load8<_Float16>(const _Float16 *p) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x8, *(const DAN_GLOBAL u32x4 *)p), f32x8);
+}
+template <>
+__device__ inline f32x8 load8<float>(const float *p) {
+  const f32x4 a = __builtin_bit_cast(f32x4, *(const DAN_GLOBAL u32x4 *)p);
+  const f32x4 b = __builtin_bit_cast(f32x4, *(const DAN_GLOBAL u32x4 *)(p + 4));
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// max |x| over the work group, in every thread.
+__device__ inline float block_amax(float v, float *red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();  // red is reused by the next call
+  return v;
+}
+
+template <typename T>
+__device__ inline float row_amax(const T *row, int cols) {
+  float a = 0.f;
+  for (int c = 8 * threadIdx.x; c < cols; c += 8 * kThreads) {
+    const f32x8 x = load8<T>(row + c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(x[i]));
+  }
+  return a;
+}
+
+__device__ inline float scale_of(float amax) { return fmaxf(amax, 1e-12f) / kE4m3Max; }
+
+template <typename T>
+__device__ inline void quantize_row(const T *row, uint8_t *out, int cols, float scale) {
+  for (int c = 8 * threadIdx.x; c < cols; c += 8 * kThreads) {
+    const f32x8 x = load8<T>(row + c);
+    u32x2 q;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h] / scale, x[4 * h + 1] / scale, 0, false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h + 2] / scale, x[4 * h + 3] / scale, w, true);
+      q[h] = (uint32_t)w;
+    }
+    *(DAN_GLOBAL u32x2 *)(out + c) = q;
+  }
+}
+
+struct Params {
+  const void *x;
+  int64_t x_stride;
+  uint8_t *xq;
+  float *scale;
+  int32_t rows, cols;
+};
+
+// Rowwise: the row's scale, then its codes.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void quant_rows_kernel(const Params p) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
+  const float s = scale_of(block_amax(row_amax<T>(row, p.cols), red));
+  if (threadIdx.x == 0) *(DAN_GLOBAL float *)(p.scale + r) = s;
+  quantize_row<T>(row, p.xq + (int64_t)r * p.cols, p.cols, s);
+}
+
+// Per tensor, step 1: zero the accumulator (scale[0] holds amax's bits until step 3).
+__global__ void zero_kernel(float *scale) { *(DAN_GLOBAL uint32_t *)scale = 0u; }
+
+// Per tensor, step 2: each row's amax into the accumulator.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void amax_rows_kernel(const Params p) {
+  __shared__ float red[4];
+  const T *row = static_cast<const T *>(p.x) + (int64_t)blockIdx.x * p.x_stride;
+  const float a = block_amax(row_amax<T>(row, p.cols), red);
+  if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned int *>(p.scale), __float_as_uint(a));
+}
+
+// Per tensor, step 3: amax -> scale.
+__global__ void finalize_kernel(float *scale) {
+  DAN_GLOBAL float *s = (DAN_GLOBAL float *)scale;
+  *s = scale_of(__uint_as_float(*(DAN_GLOBAL uint32_t *)scale));
+}
+
+// Per tensor, step 4: every row with the one scale.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void quant_tensor_kernel(const Params p) {
+  const float s = *(const DAN_GLOBAL float *)p.scale;
+  const int r = blockIdx.x;
+  quantize_row<T>(static_cast<const T *>(p.x) + (int64_t)r * p.x_stride, p.xq + (int64_t)r * p.cols, p.cols, s);
+}
+
+template <typename T>
+hipError_t launch(const Params &p, int mode, hipStream_t s) {
+  if (mode == DAN_FP8_SCALE_ROW) {
+    hipLaunchKernelGGL(quant_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(1), 0, s, p.scale);
+  hipLaunchKernelGGL(amax_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, s, p.scale);
+  hipLaunchKernelGGL(quant_tensor_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace dan_fp8
+
+extern "C" {
+
+int dan_fp8_abi_version(void) { return DAN_FP8_ABI_VERSION; }
+
+int dan_fp8_quantize(const DanFp8QuantArgs *a, void *stream) {
+  using dan::fail;
+  dan::g_err[0] = 0;
+  if (!a) return fail(DAN_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != DAN_FP8_ABI_VERSION)
+    return fail(DAN_ERR_VERSION, "abi_version %d, quantizer speaks %d", a->abi_version, DAN_FP8_ABI_VERSION);
+  if (a->dtype != DAN_DTYPE_BF16 && a->dtype != DAN_DTYPE_F16 && a->dtype != DAN_DTYPE_F32)
+    return fail(DAN_ERR_UNSUPPORTED, "dtype %d: bf16, f16 or f32", a->dtype);
+  if (a->mode != DAN_FP8_SCALE_TENSOR && a->mode != DAN_FP8_SCALE_ROW)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "mode %d: 0 (tensor) or 1 (row)", a->mode);
+  if (a->rows < 0 || a->cols < 0) return fail(DAN_ERR_INVALID_ARGUMENT, "negative shape");
+  if (a->cols % 16) return fail(DAN_ERR_INVALID_ARGUMENT, "cols %d must be a multiple of 16", a->cols);
+  if (a->rows == 0 || a->cols == 0) {  // torch's amax of an empty tensor raises; an empty row list is a no-op
+    if (a->mode == DAN_FP8_SCALE_TENSOR) return fail(DAN_ERR_INVALID_ARGUMENT, "an empty tensor has no per-tensor scale");
+    return DAN_OK;
+  }
+  if (!a->x || !a->xq || !a->scale) return fail(DAN_ERR_INVALID_ARGUMENT, "NULL pointer");
+  const int es = a->dtype == DAN_DTYPE_F32 ? 4 : 2;
+  if (a->x_stride < a->cols || ((uintptr_t)a->x & 15) || (a->x_stride * es) % 16 || ((uintptr_t)a->xq & 15) ||
+      ((uintptr_t)a->scale & 3))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with x_stride >= cols, xq 16-byte aligned");
+  dan_fp8::Params p;
+  p.x = a->x; p.x_stride = a->x_stride; p.xq = a->xq; p.scale = a->scale; p.rows = a->rows; p.cols = a->cols;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  if (a->dtype == DAN_DTYPE_BF16) err = dan_fp8::launch<__bf16>(p, a->mode, s);
+  else if (a->dtype == DAN_DTYPE_F16) err = dan_fp8::launch<_Float16>(p, a->mode, s);
+  else err = dan_fp8::launch<float>(p, a->mode, s);
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "quantizer launch failed: %s", hipGetErrorString(err));
+  return DAN_OK;
+}
+
+}  // extern "C"

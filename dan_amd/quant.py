@@ -1,0 +1,100 @@
+"""FP8 (OCP e4m3) decoder linears on gfx950, mirroring dan/quant.py.
+
+``FP8Linear`` keeps dan's module interface and conventions (dan/quant.py:23-42):
+weights quantized once, per output row (rowwise) or per tensor, activations
+quantized on every call with ``scale = max(amax, 1e-12) / 448`` and
+``xq = e4m3fn(x / scale)`` (dan/fused.py:85-91), then one scaled fp8 GEMM with
+the bias in its epilogue. The quantizer is this package's gfx950 kernel
+(``dan_fp8_quantize``, include/dan_fp8.h): one read of x per call, where
+dan's eager chain makes five passes. The GEMM is the library fp8 GEMM dan
+calls, ``torch._scaled_mm`` (dan/quant.py:40), which is hipBLASLt on gfx950
+(row and column scale vectors applied in its epilogue).
+
+There is no CPU path: CPU tensors raise (the eager CPU chain is the test
+oracle, oracle/quant.py).
+"""
+import torch
+from torch import nn
+
+from . import _native
+from .attention import _DTYPES
+
+E4M3 = torch.float8_e4m3fn
+E4M3_MAX = torch.finfo(E4M3).max  # 448 (dan/quant.py:15-16)
+
+
+def fp8_quantize(x, fp8_max=E4M3_MAX, rowwise=True):
+    """x [M, K] (bf16, fp16 or fp32, CUDA) -> (xq [M, K] e4m3fn, scale
+    [M, 1] or [1, 1] fp32), as dan/fused.py:85-91. K must be a multiple of 16
+    (dan quantizes only such linears, dan/quant.py:69-70)."""
+    if fp8_max != E4M3_MAX:
+        raise ValueError(f"fp8_max {fp8_max}: the e4m3fn maximum is {E4M3_MAX}")
+    if not x.is_cuda:
+        raise RuntimeError("dan_amd.quant.fp8_quantize runs on a gfx950 GPU only; got tensors on "
+                           f"{x.device} (the eager CPU chain is the test oracle, not a backend)")
+    if x.dim() != 2:
+        raise ValueError(f"x must be [M, K]; got {tuple(x.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"x dtype {x.dtype}: bf16, fp16 or fp32")
+    m, k = x.shape
+    es = x.element_size()
+    if x.stride(1) != 1 or x.data_ptr() % 16 or (x.stride(0) * es) % 16 or x.stride(0) < k:
+        x = x.contiguous()
+    xq = torch.empty((m, k), dtype=E4M3, device=x.device)
+    scale = torch.empty((m, 1) if rowwise else (1, 1), dtype=torch.float32, device=x.device)
+    a = _native.DanFp8QuantArgs()
+    a.abi_version = _native.FP8_ABI_VERSION
+    a.dtype = _DTYPES[x.dtype]
+    a.rows, a.cols = m, k
+    a.mode = _native.FP8_SCALE_ROW if rowwise else _native.FP8_SCALE_TENSOR
+    a.x, a.x_stride = x.data_ptr(), x.stride(0)
+    a.xq, a.scale = xq.data_ptr(), scale.data_ptr()
+    _native.fp8_quantize(a, torch.cuda.current_stream(x.device).cuda_stream)
+    return xq, scale
+
+
+def supported(device=None):
+    """gfx950 (OCP e4m3 matrix cores)."""
+    if not torch.cuda.is_available():
+        return False
+    return "gfx950" in torch.cuda.get_device_properties(device).gcnArchName
+
+
+class FP8Linear(nn.Module):
+    """dan/quant.py:23-42 on gfx950: e4m3 weight [out, in] with its scale
+    ([1, out] rowwise, [1, 1] per tensor), activations quantized per call."""
+
+    def __init__(self, linear, rowwise=True):
+        super().__init__()
+        w = linear.weight.detach()
+        self.out_features, self.in_features = w.shape
+        wq, scale = fp8_quantize(w, E4M3_MAX, rowwise)
+        self.weight = nn.Parameter(wq, requires_grad=False)  # [out, in]
+        self.register_buffer("weight_scale", scale.reshape(1, -1) if rowwise else scale)  # [1, out] or [1, 1]
+        self.bias = linear.bias
+        self.rowwise = rowwise
+        self.out_dtype = w.dtype
+
+    def forward(self, x):
+        shape = x.shape
+        xq, scale = fp8_quantize(x.reshape(-1, shape[-1]), E4M3_MAX, self.rowwise)
+        y = torch._scaled_mm(xq, self.weight.t(), scale_a=scale, scale_b=self.weight_scale,
+                             bias=self.bias, out_dtype=self.out_dtype)
+        return y.reshape(*shape[:-1], self.out_features)
+
+
+def quantize_fp8(model, min_features=16, rowwise=True):
+    """Replace the decoder's nn.Linear modules with FP8Linear in place
+    (dan/quant.py:60-73; rowwise scaling is fast on gfx950, so it is the
+    default)."""
+    device = next(model.parameters()).device
+    if not supported(device):
+        raise RuntimeError("FP8 linears need a gfx950 GPU (OCP e4m3 matrix cores)")
+    for layer in model.model.layers:
+        for mod in list(layer.modules()):
+            for name, child in list(mod.named_children()):
+                if isinstance(child, nn.Linear) and min(child.in_features, child.out_features) >= min_features \
+                        and child.in_features % 16 == 0 and child.out_features % 16 == 0:
+                    setattr(mod, name, FP8Linear(child, rowwise))
+    torch.cuda.empty_cache()
+    return model

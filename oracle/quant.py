@@ -1,0 +1,76 @@
+"""CPU oracle for the FP8 decoder linears -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/ and bench.py's cpu_baseline leg import this module, as the
+checker. The product (dan_amd.quant) never imports it and has no CPU path.
+
+- ``fp8_quantize``   dan/fused.py:85-91 restated with torch CPU ops: amax per
+                     row or per tensor, ``scale = amax.clamp(1e-12) / 448``,
+                     ``xq = (x.float() / scale).to(float8_e4m3fn)``
+- ``fp8_linear``     dan/quant.py:36-42 (FP8Linear.forward) in float64:
+                     ``(xq * scale_a) @ (wq * scale_b)^T + bias``, the exact
+                     value the scaled GEMM rounds to the model dtype, and the
+                     sum of |terms| that bounds its fp32 accumulation error
+- ``e4m3_decode``    the OCP e4m3fn value of each of the 256 codes, from the
+                     bit layout (1 sign, 4 exponent bits with bias 7, 3
+                     mantissa bits; exponent 0 subnormal; 0x7f / 0xff NaN)
+- ``e4m3_encode``    nearest e4m3fn code of each float, ties to the even
+                     mantissa, by brute force over the finite codes; pins
+                     torch's fp32 -> float8_e4m3fn cast
+"""
+import numpy as np
+import torch
+
+E4M3 = torch.float8_e4m3fn
+E4M3_MAX = 448.0
+
+
+def fp8_quantize(x, rowwise):
+    """x [M, K] (CPU) -> (xq [M, K] e4m3fn, scale [M, 1] or [1, 1] fp32)."""
+    xf = x.float()
+    amax = xf.abs().amax(dim=-1, keepdim=True) if rowwise else xf.abs().amax().reshape(1, 1)
+    scale = amax.clamp(min=1e-12) / E4M3_MAX
+    return (xf / scale).to(E4M3), scale
+
+
+def fp8_linear(xq, scale_a, wq, scale_b, bias=None):
+    """float64 value of the scaled product and the sum of |terms| (for the
+    accumulation bound): xq [M, K], scale_a [M, 1] or [1, 1], wq [N, K],
+    scale_b [1, N] or [1, 1], bias [N] or None."""
+    a = xq.double() * scale_a.double()
+    b = wq.double() * scale_b.double().reshape(-1, 1)
+    y = a @ b.t()
+    mag = a.abs() @ b.abs().t()
+    if bias is not None:
+        y = y + bias.double()
+        mag = mag + bias.double().abs()
+    return y, mag
+
+
+def e4m3_decode(codes=None):
+    """float64 value of every code in ``codes`` (default: all 256)."""
+    c = np.arange(256, dtype=np.int64) if codes is None else np.asarray(codes, np.int64)
+    s = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    v = np.where((c & 0x7F) == 0x7F, np.nan, v)
+    return s * v
+
+
+def e4m3_encode(x, chunk=4096):
+    """Nearest finite e4m3fn code of each value of ``x`` (float64 array),
+    ties to the code with the even mantissa, zero keeping x's sign; |x|
+    beyond 464 is out of range (the callers' values stay within 448)."""
+    x = np.asarray(x, np.float64).ravel()
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.int64)
+    vals = e4m3_decode(codes)
+    out = np.empty(len(x), np.int64)
+    for i in range(0, len(x), chunk):
+        xs = x[i:i + chunk]
+        d = np.abs(xs[:, None] - vals[None, :])
+        near = d == d.min(1, keepdims=True)
+        # rank the tied codes: the zero of x's sign first, then even mantissas
+        zero_ok = (vals[None, :] == 0) & (((codes[None, :] & 0x80) != 0) == np.signbit(xs)[:, None])
+        rank = np.where(near, 0, 8) + np.where(zero_ok, 0, 2) + np.where((codes & 1) == 0, 0, 1)[None, :]
+        out[i:i + chunk] = codes[np.argmin(rank, axis=1)]
+    return out

@@ -1,5 +1,5 @@
 """The C ABI without a GPU: the built library loads and exports every function
-include/dan_tree_attn.h, dan_qkv_front.h and dan_tree_plan.h declare, the ctypes mirror has the header's exact
+include/dan_tree_attn.h, dan_qkv_front.h, dan_tree_plan.h and dan_fp8.h declare, the ctypes mirror has the header's exact
 struct layout (checked by compiling the header with gcc), and argument
 errors come back as status codes with messages before any GPU call."""
 import ctypes
@@ -15,6 +15,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dan_tree_attn.h")
 FRONT_HEADER = os.path.join(ROOT, "include", "dan_qkv_front.h")
 PLAN_HEADER = os.path.join(ROOT, "include", "dan_tree_plan.h")
+FP8_HEADER = os.path.join(ROOT, "include", "dan_fp8.h")
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +28,7 @@ def lib():
 
 
 def declared_functions():
-    text = open(HEADER).read() + open(FRONT_HEADER).read() + open(PLAN_HEADER).read()
+    text = "".join(open(h).read() for h in (HEADER, FRONT_HEADER, PLAN_HEADER, FP8_HEADER))
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dan_\w+)\s*\(", text, re.M)))
 
 
@@ -50,12 +51,13 @@ STRUCTS = {
     "DanFrontSave": _native.DanFrontSave,
     "DanQkvFrontArgs": _native.DanQkvFrontArgs,
     "DanTreePlanArgs": _native.DanTreePlanArgs,
+    "DanFp8QuantArgs": _native.DanFp8QuantArgs,
 }
 
 
 def test_ctypes_layout_matches_header(tmp_path):
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', '#include "dan_qkv_front.h"',
-             '#include "dan_tree_plan.h"', "int main(void) {"]
+             '#include "dan_tree_plan.h"', '#include "dan_fp8.h"', "int main(void) {"]
     for cname, cls in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
@@ -67,6 +69,7 @@ def test_ctypes_layout_matches_header(tmp_path):
                  'DAN_FRONT_NORM_RMS_ZERO_CENTERED);')
     lines.append('printf("PLAN %d,%d,%d,%d,%d\\n", DAN_TREE_PLAN_ABI_VERSION, DAN_TREE_PLAN_MAX_WORK, '
                  'DAN_TREE_PLAN_MAX_SLOTS, DAN_TREE_PLAN_MAX_SEGMENTS, DAN_TREE_PLAN_MAX_BRANCHES);')
+    lines.append('printf("FP8 %d,%d,%d\\n", DAN_FP8_ABI_VERSION, DAN_FP8_SCALE_TENSOR, DAN_FP8_SCALE_ROW);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -84,6 +87,7 @@ def test_ctypes_layout_matches_header(tmp_path):
     assert got["PHASES"] == f"{_native.PHASES_ALL},{_native.PHASE_PACK},{_native.PHASE_ATTEND}"
     assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
                             f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
+    assert got["FP8"] == f"{_native.FP8_ABI_VERSION},{_native.FP8_SCALE_TENSOR},{_native.FP8_SCALE_ROW}"
     assert got["PLAN"] == (f"{_native.PLAN_ABI_VERSION},{_native.PLAN_MAX_WORK},{_native.PLAN_MAX_SLOTS},"
                            f"{_native.PLAN_MAX_SEGMENTS},{_native.PLAN_MAX_BRANCHES}")
 
@@ -267,3 +271,33 @@ def test_plan_empty_and_null(lib):
     assert lib.dan_tree_attn_plan(None, None) == _native.ERR_INVALID_ARGUMENT
     assert lib.dan_tree_attn_plan(ctypes.byref(_plan_args(num_work=0)), None) == _native.OK
     assert _native.last_error(lib) == ""
+
+
+def _fp8_args(**kw):
+    a = _native.DanFp8QuantArgs()
+    a.abi_version = _native.FP8_ABI_VERSION
+    a.dtype, a.rows, a.cols, a.mode, a.x_stride = _native.DTYPE_BF16, 4, 32, _native.FP8_SCALE_ROW, 32
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=3), _native.ERR_VERSION, "abi_version"),
+    (dict(dtype=_native.DTYPE_E4M3), _native.ERR_UNSUPPORTED, "dtype"),
+    (dict(mode=5), _native.ERR_INVALID_ARGUMENT, "mode"),
+    (dict(cols=24), _native.ERR_INVALID_ARGUMENT, "multiple of 16"),
+    (dict(rows=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+    (dict(rows=0, mode=_native.FP8_SCALE_TENSOR), _native.ERR_INVALID_ARGUMENT, "empty"),
+    (dict(), _native.ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(x=16, xq=16, scale=16, x_stride=8), _native.ERR_INVALID_ARGUMENT, "aligned"),
+])
+def test_fp8_argument_errors(lib, kw, status, needle):
+    rc = lib.dan_fp8_quantize(ctypes.byref(_fp8_args(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_fp8_empty_rows_is_a_no_op(lib):
+    assert lib.dan_fp8_quantize(ctypes.byref(_fp8_args(rows=0)), None) == _native.OK
+    assert lib.dan_fp8_abi_version() == _native.FP8_ABI_VERSION

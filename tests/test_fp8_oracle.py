@@ -1,0 +1,100 @@
+"""The FP8-linear oracle (oracle/quant.py) pinned without a GPU.
+
+- e4m3 decoding: every code's value from the OCP bit layout equals torch's
+  float8_e4m3fn decode.
+- e4m3 encoding: a brute-force nearest-code search (ties to the even
+  mantissa) equals torch's fp32 -> float8_e4m3fn cast on random values, on
+  every code value and its neighbours, and on every exact midpoint.
+- fp8_quantize closed forms: the row maximum maps to +-448 exactly, a row of
+  one value is all 448, a zero row keeps the 1e-12 clamp, per-tensor equals
+  rowwise on a single row, dequantization is within half an e4m3 spacing.
+- fp8_linear: the float64 product of exactly representable operands equals
+  an integer dot product computed by hand.
+- Planted mistakes (a 447 maximum, no clamp, truncation instead of rounding)
+  fail these checks."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+
+
+def torch_codes(x32):
+    return torch.from_numpy(np.ascontiguousarray(x32, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy().astype(np.int64)
+
+
+def test_decode_every_code_matches_torch():
+    dec = Q.e4m3_decode()
+    t = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).double().numpy()
+    assert np.array_equal(np.isnan(dec), np.isnan(t))
+    ok = ~np.isnan(dec)
+    assert np.array_equal(dec[ok], t[ok])
+    assert dec[0x7E] == 448.0 and dec[0x01] == 2.0 ** -9 and dec[0x08] == 2.0 ** -6
+
+
+def test_encode_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    dec = Q.e4m3_decode()
+    fin = dec[np.isfinite(dec)]
+    mids = (np.sort(fin)[1:] + np.sort(fin)[:-1]) / 2
+    x = np.concatenate([rng.standard_normal(8000) * 100, rng.standard_normal(8000) * 0.02, fin, np.nextafter(fin, 1e9),
+                        np.nextafter(fin, -1e9), mids, [0.0, -0.0, 1e-30, -1e-30]])
+    x32 = x[np.abs(x) <= 448].astype(np.float32)
+    assert np.array_equal(Q.e4m3_encode(x32.astype(np.float64)), torch_codes(x32))
+
+
+def test_planted_truncation_fails_the_encode_pin():
+    x = np.array([1.0625, 1.1875, 3.3], np.float64)  # 1.0625 is a tie between 1.0 and 1.125
+    dec = Q.e4m3_decode()
+    trunc = np.array([max(c for c in range(0x7F) if dec[c] <= v) for v in x])
+    assert not np.array_equal(trunc, torch_codes(x.astype(np.float32)))
+
+
+def test_quantize_closed_forms():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, 64, generator=g) * 3
+    xq, s = Q.fp8_quantize(x, rowwise=True)
+    amax = x.abs().amax(1)
+    assert torch.equal(s.squeeze(1), amax.clamp(min=1e-12) / 448.0)
+    arg = x.abs().argmax(1)
+    top = xq.float()[torch.arange(5), arg]
+    assert torch.equal(top.abs(), torch.full((5,), 448.0))
+    assert torch.equal(torch.sign(top), torch.sign(x[torch.arange(5), arg]))
+    deq = xq.double() * s.double()
+    # within half an e4m3 spacing: 2^(e-3) / 2 for |v| in [2^e, 2^(e+1)), 2^-10 below 2^-6
+    v = (x.double() / s.double()).abs()
+    e = torch.floor(torch.log2(torch.clamp(v, min=2.0 ** -6)))
+    half = torch.where(v >= 2.0 ** -6, 2.0 ** (e - 4), torch.full_like(v, 2.0 ** -10))
+    assert ((deq - x.double()).abs() <= half * s.double() * (1 + 1e-12)).all()
+    one = torch.full((2, 32), -0.75)
+    q1, s1 = Q.fp8_quantize(one, rowwise=True)
+    assert torch.equal(q1.float(), torch.full((2, 32), -448.0))
+    z, sz = Q.fp8_quantize(torch.zeros(1, 16), rowwise=False)
+    assert torch.equal(sz, torch.full((1, 1), 1e-12) / 448.0) and torch.equal(z.float(), torch.zeros(1, 16))
+    r = torch.randn(1, 48, generator=g)
+    a, sa = Q.fp8_quantize(r, rowwise=True)
+    b, sb = Q.fp8_quantize(r, rowwise=False)
+    assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)) and torch.equal(sa, sb)
+
+
+def test_planted_scale_mistakes_fail():
+    x = torch.tensor([[68.1, -448.0, 0.5, 7.0] * 4])  # 68.1 -> 72 with 448, 67.95 -> 64 with 447
+    xq, _ = Q.fp8_quantize(x, rowwise=True)
+    assert xq.float()[0, 0] == 72.0
+    wrong = ((x / (x.abs().amax() / 447.0)).to(torch.float8_e4m3fn))
+    assert not torch.equal(wrong.view(torch.uint8), xq.view(torch.uint8))
+    _, s0 = Q.fp8_quantize(torch.zeros(1, 16), rowwise=True)
+    assert torch.isfinite(s0).all() and (s0 > 0).all()  # without the clamp the scale is 0 and xq NaN
+
+
+def test_linear_exact_small_case():
+    xq = torch.tensor([[1.0, 2.0, -0.5], [0.25, 0.0, 448.0]]).to(torch.float8_e4m3fn)
+    wq = torch.tensor([[3.0, -1.0, 2.0], [0.5, 0.5, 0.5]]).to(torch.float8_e4m3fn)
+    sa = torch.tensor([[2.0], [0.5]])
+    sb = torch.tensor([[1.0, 4.0]])
+    bias = torch.tensor([1.0, -1.0])
+    y, mag = Q.fp8_linear(xq, sa, wq, sb, bias)
+    want = torch.tensor([[2 * (3 - 2 - 1) * 1 + 1, 2 * (0.5 + 1 - 0.25) * 4 - 1],
+                         [0.5 * (0.75 + 0 + 896) * 1 + 1, 0.5 * (0.125 + 0 + 224) * 4 - 1]], dtype=torch.float64)
+    assert torch.equal(y, want)
+    assert (mag >= y.abs()).all()
