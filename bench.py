@@ -262,6 +262,91 @@ def bench_fp8_linear(args):
     }), flush=True)
 
 
+def bench_gdn(args):
+    """The Gated DeltaNet recurrence of one layer over the c3 tree batch, as
+    dan/models/qwen3_5.py:198-210 phases it: every trunk from its segment's
+    state (the prefix cache's state for a segment with a past, else zeros),
+    then every branch from its trunk's final state. Head shape: 16 key and
+    16 value heads of 128 (a Qwen3.5-style DeltaNet layer); synthetic
+    post-convolution q, k, v and gates. One step = the two phase calls."""
+    from dan_amd import workloads
+    from dan_amd.deltanet import delta_rule
+
+    dev = torch.device("cuda:0")
+    w = workloads.config3(args.seed, device="cpu")
+    hk = hv = 16
+    d = 128
+    trunks = [(s.start, s.trunk) for s in w.segments]
+    branches = [(a, b - a, i) for i, s in enumerate(w.segments) for a, b in s.branches]
+    n = w.num_tokens
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn(n, hk, d, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, hk, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hv, d, device=dev, generator=g).to(torch.bfloat16)
+    gate = -(torch.rand(n, hv, device=dev, generator=g) * 0.1)
+    beta = torch.rand(n, hv, device=dev, generator=g)
+    init = torch.randn(len(trunks), hv, d, d, device=dev, generator=g) * 0.05
+    trow = torch.cat([torch.arange(a, a + t) for a, t in trunks]).to(dev)
+    brow = torch.cat([torch.arange(a, a + m) for a, m, _ in branches]).to(dev)
+    bseg = torch.tensor([i for _, _, i in branches], device=dev)
+    tl, bl = [t for _, t in trunks], [m for _, m, _ in branches]
+    out = torch.empty(n, hv, d, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        ot, ft = delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init)
+        out[trow] = ot
+        ob, _ = delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, ft.index_select(0, bseg))
+        out[brow] = ob
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t) / args.steps
+    ft = delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init)[1]
+    bst = ft.index_select(0, bseg)
+    tr_ms = _event_ms(lambda: delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init), args.steps)
+    br_ms = _event_ms(lambda: delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, bst), args.steps)
+    tokens = len(trow) + len(brow)
+    flops = tokens * hv * 7 * d * d  # per token and head: decay, S^T k, the rank-1 write, S^T q
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import deltanet as OD
+        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        ct = [x.cpu()[trow.cpu()] for x in (q, k, v, gate, beta)]
+        cb = [x.cpu()[brow.cpu()] for x in (q, k, v, gate, beta)]
+        init_c, bseg_c = init.cpu(), bseg.cpu()
+        reps, tc = 0, time.perf_counter()
+        while True:  # whole layer steps, both phases, until about 5 s of CPU work
+            fc = OD.delta_rule(*ct, tl, init_c)[1]
+            OD.delta_rule(*cb, bl, fc.index_select(0, bseg_c))
+            reps += 1
+            if time.perf_counter() - tc > 5.0:
+                break
+        tc = time.perf_counter() - tc
+        cpu = {"value": round(reps * tokens / tc, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{reps} whole layer steps ({tokens} tokens x {hv} heads, trunk then branch phase) through "
+                         f"the oracle's chunked form (the reference's delta_rule_torch restated, fp32): {tc:.2f} s; "
+                         f"CPU: {cpu_model()}"}
+    print(json.dumps({
+        "metric": "Gated DeltaNet recurrence, one layer over the c3 tree batch, tokens/s, 1 GPU",
+        "value": round(tokens / wall, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 state, bf16 io", "data": "synthetic",
+        "config": {"workload": f"gdn-c3: {len(trunks)} trunks (longest {max(tl)}), {len(bl)} branches, {tokens} tokens, "
+                               f"{hk}/{hv} heads, Dk = Dv = {d}", "seed": args.seed},
+        "roofline": {"bound": "fp32 VALU (sequential per run)", "achieved": round(flops / wall / 1e12, 2),
+                     "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
+                     "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4),
+                     "longest_run_tokens": max(tl), "us_per_token_longest_run": round(tr_ms * 1e3 / max(tl), 3)},
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
 def bench_plan(args):
     """Per-forward tile planning: the host planner (numpy tables, schedule
     and uploads) against the device planner (O(segments) host part, one
@@ -328,6 +413,8 @@ def main():
                          "instead of the attention")
     ap.add_argument("--fp8-linear", action="store_true",
                     help="measure one Llama-3-8B decoder layer's FP8 linears (quantize + hipBLASLt GEMM) at 8192 tokens")
+    ap.add_argument("--gdn", action="store_true",
+                    help="measure the Gated DeltaNet recurrence of one layer over the c3 tree batch")
     ap.add_argument("--plan", action="store_true",
                     help="measure per-forward tile planning (host planner against the device planner) on --workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -350,6 +437,9 @@ def main():
         return
     if args.fp8_linear:
         bench_fp8_linear(args)
+        return
+    if args.gdn:
+        bench_gdn(args)
         return
     if args.front:
         if args.workload not in FRONT_SHAPES:

@@ -1,5 +1,6 @@
 """ctypes binding of the C ABI in include/dan_tree_attn.h (with
-include/dan_qkv_front.h, include/dan_tree_plan.h and include/dan_fp8.h).
+include/dan_qkv_front.h, include/dan_tree_plan.h, include/dan_fp8.h and
+include/dan_gdn.h).
 
 The shared library is plain C ABI (no torch types), built in-tree by
 ``dan_amd._build`` into ``dan_amd/_lib/``. It must be loaded after torch has
@@ -115,10 +116,24 @@ class DanFp8QuantArgs(ctypes.Structure):
                 ("reserved", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
 
 
+GDN_ABI_VERSION = 1
+
+
+class DanGdnArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("dtype", _i32), ("num_k_heads", _i32), ("num_v_heads", _i32), ("k_dim", _i32),
+                ("v_dim", _i32), ("num_runs", _i32), ("num_tokens", _i32), ("cu", _vp),
+                ("q", _vp), ("q_stride_tok", _i64), ("q_stride_head", _i64),
+                ("k", _vp), ("k_stride_tok", _i64), ("k_stride_head", _i64),
+                ("v", _vp), ("v_stride_tok", _i64), ("v_stride_head", _i64),
+                ("g", _vp), ("beta", _vp), ("states_in", _vp), ("states_out", _vp),
+                ("out", _vp), ("o_stride_tok", _i64), ("o_stride_head", _i64),
+                ("workspace", _vp), ("workspace_bytes", _i64)]
+
+
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
            "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
-           "dan_fp8_quantize", "dan_fp8_abi_version")
+           "dan_fp8_quantize", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version")
 
 _lock = threading.Lock()
 _lib = None
@@ -162,11 +177,17 @@ def load(path=LIB_PATH):
         lib.dan_fp8_quantize.restype = ctypes.c_int
         lib.dan_fp8_abi_version.argtypes = []
         lib.dan_fp8_abi_version.restype = ctypes.c_int
+        lib.dan_gdn_fwd.argtypes = [ctypes.POINTER(DanGdnArgs), _vp]
+        lib.dan_gdn_fwd.restype = ctypes.c_int
+        lib.dan_gdn_workspace_size.argtypes = [_i32, _i32]
+        lib.dan_gdn_workspace_size.restype = _i64
+        lib.dan_gdn_abi_version.argtypes = []
+        lib.dan_gdn_abi_version.restype = ctypes.c_int
         got = (lib.dan_tree_attn_abi_version(), lib.dan_qkv_front_abi_version(), lib.dan_tree_attn_plan_abi_version(),
-               lib.dan_fp8_abi_version())
-        want = (ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION, FP8_ABI_VERSION)
+               lib.dan_fp8_abi_version(), lib.dan_gdn_abi_version())
+        want = (ABI_VERSION, FRONT_ABI_VERSION, PLAN_ABI_VERSION, FP8_ABI_VERSION, GDN_ABI_VERSION)
         if got != want:
-            raise RuntimeError(f"{path} speaks ABI versions {got} (attention, front end, planner, fp8), this package "
+            raise RuntimeError(f"{path} speaks ABI versions {got} (attention, front end, planner, fp8, delta rule), this package "
                                f"{want}; rebuild it")
         if path == LIB_PATH:
             _lib = lib
@@ -228,3 +249,11 @@ def fp8_quantize(args, stream, lib=None):
     rc = lib.dan_fp8_quantize(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_fp8_quantize failed ({rc}): {last_error(lib)}")
+
+
+def gdn(args, stream, lib=None):
+    """Launch the gated delta rule; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_gdn_fwd(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_gdn_fwd failed ({rc}): {last_error(lib)}")

@@ -1,0 +1,272 @@
+// Gated delta rule (Gated DeltaNet recurrence) over packed runs on gfx950
+// (MI355X, CDNA4): dan/models/qwen3_5.py:136-158 (delta_rule), token by
+// token in fp32 from each run's initial state.
+//
+// Two launches:
+//   gdn_norms_kernel  one wave per (token, key head): 1 / sqrt(sum(x^2) + 1e-6)
+//                     of q and of k (dan/models/qwen3_5.py:99-100), into the
+//                     caller's workspace -- the reductions leave the
+//                     sequential loop.
+//   gdn_kernel        one wave per (run, value head, block of 8 state columns);
+//                     lane 8 e + c owns rows 16 e .. 16 e + 15 of column c of
+//                     the state S [Dk = 128, Dv] (16 fp32 registers), so every
+//                     wave walks its run alone, without barriers. Per token,
+//                     with its inputs loaded four tokens ahead (the lane's 16
+//                     rows of q and k, v, g, beta and the two norm factors):
+//                       q' = (q r_q) Dk^-1/2, k' = k r_k      (fp32)
+//                       S <- exp(g) S;  u = S^T k' (two chains of 8 products,
+//                       then the eight row blocks summed by three VALU lane
+//                       exchanges, sum_rows8);  S <- S + k' (beta (v - u))^T;
+//                       o = S^T q' (likewise); row block 0 writes o.
+// The recurrence is sequential in the tokens of a run; its critical path per
+// token is one load-free chain of about 30 dependent operations.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "dan_gdn.h"
+
+namespace dan {
+int fail(int status, const char *fmt, ...);  // tree_attn.hip: sets the thread's last-error message
+extern thread_local char g_err[512];
+}  // namespace dan
+
+namespace dan_gdn {
+
+constexpr int kDk = 128;
+constexpr int kWavesPerGroup = 4;
+constexpr int kAhead = 4;  // tokens loaded ahead (the FIFO depth)
+constexpr int kCols = 8;   // state columns per wave
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+#define DAN_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+struct V;
+template <>
+struct V<__bf16> {
+  typedef bf16x4 x4;
+  typedef bf16x8 x8;
+};
+template <>
+struct V<_Float16> {
+  typedef f16x4 x4;
+  typedef f16x8 x8;
+};
+
+template <typename T>
+__device__ inline f32x4 cvt4(u32x2 raw) {
+  return __builtin_convertvector(__builtin_bit_cast(typename V<T>::x4, raw), f32x4);
+}
+template <typename T>
+__device__ inline f32x8 cvt8(u32x4 raw) {
+  return __builtin_convertvector(__builtin_bit_cast(typename V<T>::x8, raw), f32x8);
+}
+
+struct Params {
+  const int32_t *cu;
+  const void *q, *k, *v;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+  const float *g, *beta, *s_in;
+  float *s_out;
+  void *o;
+  float *norms;  // [N][Hk][2]: 1 / sqrt(sum q^2 + eps), 1 / sqrt(sum k^2 + eps)
+  int32_t N, Hk, Hv, Dv, R, cblocks;
+};
+
+// One wave per (token, key head): lanes 0-31 hold 4 values of q, 32-63 of k.
+template <typename T>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_norms_kernel(const Params p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6);
+  if (item >= (int64_t)p.N * p.Hk) return;
+  const int n = (int)(item / p.Hk), hk = (int)(item % p.Hk);
+  const T *src = lane < 32 ? static_cast<const T *>(p.q) + (int64_t)n * p.q_st + (int64_t)hk * p.q_sh
+                           : static_cast<const T *>(p.k) + (int64_t)n * p.k_st + (int64_t)hk * p.k_sh;
+  const f32x4 x = cvt4<T>(*(const DAN_GLOBAL u32x2 *)(src + 4 * (lane & 31)));
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+  for (int m = 1; m <= 16; m <<= 1) ss += __shfl_xor(ss, m);
+  if ((lane & 31) == 0) *(DAN_GLOBAL float *)(p.norms + item * 2 + (lane >> 5)) = 1.0f / sqrtf(ss + 1e-6f);
+}
+
+// Sum of x over the 8 lanes l with the same l % 8 (lanes l, l + 8, .., l + 56),
+// in every lane, on the VALU: a DPP rotation by 8 within each row of 16 lanes,
+// then the row swap (v_permlane16_swap) and the half swap (v_permlane32_swap).
+__device__ inline float sum_rows8(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+                                                             0x128, 0xf, 0xf, false));
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __builtin_bit_cast(float, (uint32_t)r16[0]) + __builtin_bit_cast(float, (uint32_t)r16[1]);
+  u = __builtin_bit_cast(uint32_t, x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r32[0]) + __builtin_bit_cast(float, (uint32_t)r32[1]);
+}
+
+// One token's inputs, loaded ahead.
+struct Slot {
+  u32x4 q0, q1, k0, k1;  // the lane's 16 rows of q and of k
+  float v, g, b, rq, rk;
+};
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * kWavesPerGroup + wave;  // (run, head, column block)
+  if (unit >= p.R * p.Hv * p.cblocks) return;           // whole waves only: no barrier follows
+  const int cb = unit % p.cblocks, h = (unit / p.cblocks) % p.Hv, r = unit / (p.cblocks * p.Hv);
+  const int hk = h / (p.Hv / p.Hk);
+  const int re = lane >> 3, c = kCols * cb + (lane & 7);
+  const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r);
+  const int len = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1) - row0;
+
+  // state rows 16 re .. 16 re + 15 of column c
+  const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + c;
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(16 * re + i) * p.Dv);
+
+  const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh + 16 * re;
+  const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh + 16 * re;
+  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + c;
+  auto load = [&](int t) __attribute__((always_inline)) {
+    Slot sl;
+    const int64_t row = row0 + t;
+    const DAN_GLOBAL u32x4 *qs = (const DAN_GLOBAL u32x4 *)(qh + row * p.q_st);
+    const DAN_GLOBAL u32x4 *ks = (const DAN_GLOBAL u32x4 *)(kh + row * p.k_st);
+    sl.q0 = qs[0];
+    sl.q1 = qs[1];
+    sl.k0 = ks[0];
+    sl.k1 = ks[1];
+    sl.v = (float)*(const DAN_GLOBAL T *)(vh + row * p.v_st);
+    sl.g = *(const DAN_GLOBAL float *)(p.g + row * p.Hv + h);
+    sl.b = *(const DAN_GLOBAL float *)(p.beta + row * p.Hv + h);
+    const DAN_GLOBAL float *nr = (const DAN_GLOBAL float *)(p.norms + (row * p.Hk + hk) * 2);
+    sl.rq = nr[0];
+    sl.rk = nr[1];
+    return sl;
+  };
+  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + c;
+  const float qscale = 0.08838834764831845f;  // Dk^-1/2 (dan/models/qwen3_5.py:110)
+
+  auto step = [&](int t, const Slot &sl) __attribute__((always_inline)) {
+    const f32x8 qa = cvt8<T>(sl.q0), qb = cvt8<T>(sl.q1), ka = cvt8<T>(sl.k0), kb = cvt8<T>(sl.k1);
+    float qv[16], kv[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qv[e] = (qa[e] * sl.rq) * qscale;
+      qv[8 + e] = (qb[e] * sl.rq) * qscale;
+      kv[e] = ka[e] * sl.rk;
+      kv[8 + e] = kb[e] * sl.rk;
+    }
+    const float a = expf(sl.g);
+    float u0 = 0.f, u1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i] *= a;
+      s[8 + i] *= a;
+      u0 = fmaf(kv[i], s[i], u0);
+      u1 = fmaf(kv[8 + i], s[8 + i], u1);
+    }
+    const float u = sum_rows8(u0 + u1);
+    const float w = sl.b * (sl.v - u);
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i] = fmaf(kv[i], w, s[i]);
+      s[8 + i] = fmaf(kv[8 + i], w, s[8 + i]);
+      o0 = fmaf(qv[i], s[i], o0);
+      o1 = fmaf(qv[8 + i], s[8 + i], o1);
+    }
+    const float o = sum_rows8(o0 + o1);
+    if (re == 0) *(DAN_GLOBAL T *)(oh + (int64_t)(row0 + t) * p.o_st) = (T)o;
+  };
+
+  Slot f[kAhead];
+#pragma unroll
+  for (int j = 0; j < kAhead; ++j)
+    if (j < len) f[j] = load(j);
+  for (int t = 0; t < len; t += kAhead) {
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) {
+      if (t + j < len) {
+        const Slot cur = f[j];
+        if (t + j + kAhead < len) f[j] = load(t + j + kAhead);
+        step(t + j, cur);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(16 * re + i) * p.Dv) = s[i];
+}
+
+}  // namespace dan_gdn
+
+extern "C" {
+
+int dan_gdn_abi_version(void) { return DAN_GDN_ABI_VERSION; }
+
+int64_t dan_gdn_workspace_size(int32_t num_tokens, int32_t num_k_heads) {
+  if (num_tokens < 0 || num_k_heads <= 0) return 0;
+  return ((int64_t)num_tokens * num_k_heads * 2 * 4 + 255) / 256 * 256;
+}
+
+int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
+  using dan::fail;
+  dan::g_err[0] = 0;
+  if (!a) return fail(DAN_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != DAN_GDN_ABI_VERSION)
+    return fail(DAN_ERR_VERSION, "abi_version %d, delta rule speaks %d", a->abi_version, DAN_GDN_ABI_VERSION);
+  if (a->dtype != DAN_DTYPE_BF16 && a->dtype != DAN_DTYPE_F16) return fail(DAN_ERR_UNSUPPORTED, "dtype %d: bf16 or f16", a->dtype);
+  if (a->k_dim != 128) return fail(DAN_ERR_UNSUPPORTED, "k_dim %d: only 128 is built", a->k_dim);
+  if (a->v_dim <= 0 || a->v_dim % 8 || a->v_dim > 256) return fail(DAN_ERR_UNSUPPORTED, "v_dim %d: a multiple of 8 up to 256", a->v_dim);
+  if (a->num_k_heads <= 0 || a->num_v_heads <= 0 || a->num_v_heads % a->num_k_heads)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "num_v_heads %d must be a positive multiple of num_k_heads %d", a->num_v_heads,
+                a->num_k_heads);
+  if (a->num_runs < 0 || a->num_tokens < 0) return fail(DAN_ERR_INVALID_ARGUMENT, "negative run or token count");
+  if (a->num_runs == 0) return DAN_OK;
+  if (!a->cu || !a->q || !a->k || !a->v || !a->g || !a->beta || !a->states_in || !a->states_out || !a->out ||
+      !a->workspace)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) || (a->q_stride_tok % 8) || (a->q_stride_head % 8) ||
+      (a->k_stride_tok % 8) || (a->k_stride_head % 8))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "q and k rows must be 16-byte aligned");
+  if (a->workspace_bytes < dan_gdn_workspace_size(a->num_tokens, a->num_k_heads) || ((uintptr_t)a->workspace & 15))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "workspace needs %lld bytes, 16-byte aligned",
+                (long long)dan_gdn_workspace_size(a->num_tokens, a->num_k_heads));
+  const int64_t units = (int64_t)a->num_runs * a->num_v_heads * (a->v_dim / dan_gdn::kCols);
+  const int64_t grid = (units + dan_gdn::kWavesPerGroup - 1) / dan_gdn::kWavesPerGroup;
+  if (grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "too many runs x heads");
+  dan_gdn::Params p;
+  p.cu = a->cu; p.q = a->q; p.k = a->k; p.v = a->v;
+  p.q_st = a->q_stride_tok; p.q_sh = a->q_stride_head; p.k_st = a->k_stride_tok; p.k_sh = a->k_stride_head;
+  p.v_st = a->v_stride_tok; p.v_sh = a->v_stride_head; p.o_st = a->o_stride_tok; p.o_sh = a->o_stride_head;
+  p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
+  p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
+  p.cblocks = a->v_dim / dan_gdn::kCols; p.N = a->num_tokens; p.norms = static_cast<float *>(a->workspace);
+  const int64_t ngrid = ((int64_t)a->num_tokens * a->num_k_heads + dan_gdn::kWavesPerGroup - 1) / dan_gdn::kWavesPerGroup;
+  if (ngrid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "too many tokens x heads");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 block(64 * dan_gdn::kWavesPerGroup);
+  if (a->dtype == DAN_DTYPE_BF16) {
+    if (ngrid) hipLaunchKernelGGL(dan_gdn::gdn_norms_kernel<__bf16>, dim3((unsigned)ngrid), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdn::gdn_kernel<__bf16>, dim3((unsigned)grid), block, 0, s, p);
+  } else {
+    if (ngrid) hipLaunchKernelGGL(dan_gdn::gdn_norms_kernel<_Float16>, dim3((unsigned)ngrid), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdn::gdn_kernel<_Float16>, dim3((unsigned)grid), block, 0, s, p);
+  }
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "delta rule launch failed: %s", hipGetErrorString(err));
+  return DAN_OK;
+}
+
+}  // extern "C"

@@ -1,5 +1,5 @@
 """The C ABI without a GPU: the built library loads and exports every function
-include/dan_tree_attn.h, dan_qkv_front.h, dan_tree_plan.h and dan_fp8.h declare, the ctypes mirror has the header's exact
+include/dan_tree_attn.h, dan_qkv_front.h, dan_tree_plan.h, dan_fp8.h and dan_gdn.h declare, the ctypes mirror has the header's exact
 struct layout (checked by compiling the header with gcc), and argument
 errors come back as status codes with messages before any GPU call."""
 import ctypes
@@ -16,6 +16,7 @@ HEADER = os.path.join(ROOT, "include", "dan_tree_attn.h")
 FRONT_HEADER = os.path.join(ROOT, "include", "dan_qkv_front.h")
 PLAN_HEADER = os.path.join(ROOT, "include", "dan_tree_plan.h")
 FP8_HEADER = os.path.join(ROOT, "include", "dan_fp8.h")
+GDN_HEADER = os.path.join(ROOT, "include", "dan_gdn.h")
 
 
 @pytest.fixture(scope="module")
@@ -28,7 +29,7 @@ def lib():
 
 
 def declared_functions():
-    text = "".join(open(h).read() for h in (HEADER, FRONT_HEADER, PLAN_HEADER, FP8_HEADER))
+    text = "".join(open(h).read() for h in (HEADER, FRONT_HEADER, PLAN_HEADER, FP8_HEADER, GDN_HEADER))
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dan_\w+)\s*\(", text, re.M)))
 
 
@@ -52,12 +53,13 @@ STRUCTS = {
     "DanQkvFrontArgs": _native.DanQkvFrontArgs,
     "DanTreePlanArgs": _native.DanTreePlanArgs,
     "DanFp8QuantArgs": _native.DanFp8QuantArgs,
+    "DanGdnArgs": _native.DanGdnArgs,
 }
 
 
 def test_ctypes_layout_matches_header(tmp_path):
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dan_tree_attn.h"', '#include "dan_qkv_front.h"',
-             '#include "dan_tree_plan.h"', '#include "dan_fp8.h"', "int main(void) {"]
+             '#include "dan_tree_plan.h"', '#include "dan_fp8.h"', '#include "dan_gdn.h"', "int main(void) {"]
     for cname, cls in STRUCTS.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
@@ -70,6 +72,7 @@ def test_ctypes_layout_matches_header(tmp_path):
     lines.append('printf("PLAN %d,%d,%d,%d,%d\\n", DAN_TREE_PLAN_ABI_VERSION, DAN_TREE_PLAN_MAX_WORK, '
                  'DAN_TREE_PLAN_MAX_SLOTS, DAN_TREE_PLAN_MAX_SEGMENTS, DAN_TREE_PLAN_MAX_BRANCHES);')
     lines.append('printf("FP8 %d,%d,%d\\n", DAN_FP8_ABI_VERSION, DAN_FP8_SCALE_TENSOR, DAN_FP8_SCALE_ROW);')
+    lines.append('printf("GDN %d\\n", DAN_GDN_ABI_VERSION);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -88,6 +91,7 @@ def test_ctypes_layout_matches_header(tmp_path):
     assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
                             f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
     assert got["FP8"] == f"{_native.FP8_ABI_VERSION},{_native.FP8_SCALE_TENSOR},{_native.FP8_SCALE_ROW}"
+    assert int(got["GDN"]) == _native.GDN_ABI_VERSION
     assert got["PLAN"] == (f"{_native.PLAN_ABI_VERSION},{_native.PLAN_MAX_WORK},{_native.PLAN_MAX_SLOTS},"
                            f"{_native.PLAN_MAX_SEGMENTS},{_native.PLAN_MAX_BRANCHES}")
 
@@ -301,3 +305,32 @@ def test_fp8_argument_errors(lib, kw, status, needle):
 def test_fp8_empty_rows_is_a_no_op(lib):
     assert lib.dan_fp8_quantize(ctypes.byref(_fp8_args(rows=0)), None) == _native.OK
     assert lib.dan_fp8_abi_version() == _native.FP8_ABI_VERSION
+
+
+def _gdn_args(**kw):
+    a = _native.DanGdnArgs()
+    a.abi_version = _native.GDN_ABI_VERSION
+    a.dtype, a.num_k_heads, a.num_v_heads, a.k_dim, a.v_dim, a.num_runs = _native.DTYPE_BF16, 2, 4, 128, 128, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=9), _native.ERR_VERSION, "abi_version"),
+    (dict(dtype=_native.DTYPE_F32), _native.ERR_UNSUPPORTED, "dtype"),
+    (dict(k_dim=64), _native.ERR_UNSUPPORTED, "k_dim"),
+    (dict(v_dim=36), _native.ERR_UNSUPPORTED, "v_dim"),
+    (dict(num_v_heads=3), _native.ERR_INVALID_ARGUMENT, "multiple"),
+    (dict(num_runs=-2), _native.ERR_INVALID_ARGUMENT, "negative"),
+    (dict(), _native.ERR_INVALID_ARGUMENT, "NULL"),
+])
+def test_gdn_argument_errors(lib, kw, status, needle):
+    rc = lib.dan_gdn_fwd(ctypes.byref(_gdn_args(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_gdn_no_runs_is_a_no_op(lib):
+    assert lib.dan_gdn_fwd(ctypes.byref(_gdn_args(num_runs=0)), None) == _native.OK
+    assert lib.dan_gdn_abi_version() == _native.GDN_ABI_VERSION

@@ -1,0 +1,104 @@
+"""The gfx950 gated delta rule (dan_amd.deltanet.delta_rule -> dan_gdn_fwd)
+against the float64 token-by-token oracle (oracle/deltanet.py), which the
+CPU tests pin against the restated chunked form and closed forms.
+
+Bars (fp32 state, outputs rounded to the model dtype):
+- outputs within 2^-8 of |reference| + 2e-3 (bf16; 2^-11 and 5e-4 for fp16);
+- final states within 1e-4 + 1e-4 |reference|;
+- splitting a run into two calls, the second from the first's final state,
+  is bit-identical to one call (the kernel's arithmetic per token does not
+  depend on where a run starts);
+- the tree phases (trunk part 1, part 2 from its states, branches from the
+  trunk's final state) equal the oracle run over each root-to-leaf path."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from dan_amd.deltanet import delta_rule
+from oracle import deltanet as OD
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def inputs(lengths, hk, hv, dv, dtype, gpu, seed):
+    g = torch.Generator().manual_seed(seed)
+    n = sum(lengths)
+    q = torch.randn(n, hk, 128, generator=g).to(dtype)
+    k = torch.randn(n, hk, 128, generator=g).to(dtype)
+    v = torch.randn(n, hv, dv, generator=g).to(dtype)
+    gg = -(torch.rand(n, hv, generator=g) * 0.3 + 0.01)
+    b = torch.rand(n, hv, generator=g)
+    st = torch.randn(len(lengths), hv, 128, dv, generator=g) * 0.1
+    return [x.to(gpu) for x in (q, k, v, gg, b, st)]
+
+
+def check(out, fin, ref_o, ref_f, dtype):
+    rel, ab = (2.0 ** -8, 2e-3) if dtype == torch.bfloat16 else (2.0 ** -11, 5e-4)
+    eo = (out.cpu().double() - ref_o.double()).abs()
+    ef = (fin.cpu().double() - ref_f.double()).abs()
+    say(f"  max |out - ref| {eo.max().item():.3e}, max |state - ref| {ef.max().item():.3e}")
+    assert (eo <= rel * ref_o.double().abs() + ab).all()
+    assert (ef <= 1e-4 + 1e-4 * ref_f.double().abs()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hk,hv,dv", [(2, 2, 128), (2, 4, 128), (1, 3, 64)])
+def test_delta_rule_matches_oracle(gpu, dtype, hk, hv, dv):
+    lengths = [5, 0, 1, 300, 64, 17]
+    say(f"delta rule {dtype} Hk {hk} Hv {hv} Dv {dv} runs {lengths}")
+    q, k, v, g, b, st = inputs(lengths, hk, hv, dv, dtype, gpu, seed=hk * 10 + hv + dv)
+    out, fin = delta_rule(q, k, v, g, b, lengths, st)
+    torch.cuda.synchronize()
+    ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), lengths, st.cpu(), recurrent=True)
+    check(out, fin, ref_o, ref_f, dtype)
+    assert torch.equal(fin[1], st[1])  # empty run: state unchanged
+
+
+def test_split_run_is_bit_identical(gpu):
+    say("delta rule: one run of 400 tokens vs two calls (150 + 250)")
+    q, k, v, g, b, st = inputs([400], 2, 2, 128, torch.bfloat16, gpu, seed=1)
+    out, fin = delta_rule(q, k, v, g, b, [400], st)
+    o1, f1 = delta_rule(q[:150], k[:150], v[:150], g[:150], b[:150], [150], st)
+    o2, f2 = delta_rule(q[150:], k[150:], v[150:], g[150:], b[150:], [250], f1)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([o1, o2]), out) and torch.equal(f2, fin)
+
+
+def test_tree_phases_equal_paths(gpu):
+    """Trunk of 200 tokens saved at 120 (two parts), two branches of 30 and 7
+    tokens: phase calls as dan/models/qwen3_5.py:198-210 makes them."""
+    say("delta rule: tree phases vs root-to-leaf paths")
+    trunk, cut, br = 200, 120, [30, 7]
+    n = trunk + sum(br)
+    q, k, v, g, b, st = inputs([n], 2, 2, 128, torch.bfloat16, gpu, seed=4)
+    o = torch.empty(n, 2, 128, dtype=torch.bfloat16, device=gpu)
+    o[:cut], f1 = delta_rule(q[:cut], k[:cut], v[:cut], g[:cut], b[:cut], [cut], st)
+    o[cut:trunk], f2 = delta_rule(q[cut:trunk], k[cut:trunk], v[cut:trunk], g[cut:trunk], b[cut:trunk], [trunk - cut], f1)
+    rows = slice(trunk, n)
+    ob, fb = delta_rule(q[rows], k[rows], v[rows], g[rows], b[rows], br, f2.expand(len(br), -1, -1, -1).contiguous())
+    o[rows] = ob
+    torch.cuda.synchronize()
+    c = [x.cpu() for x in (q, k, v, g, b)]
+    at = trunk
+    for i, nb in enumerate(br):
+        idx = torch.cat([torch.arange(trunk), torch.arange(at, at + nb)])
+        ref_o, ref_f = OD.delta_rule(*(x[idx] for x in c), [trunk + nb], st.cpu(), recurrent=True)
+        check(torch.cat([o[:trunk], o[at:at + nb]]), fb[i:i + 1], ref_o, ref_f, torch.bfloat16)
+        at += nb
+
+
+def test_errors(gpu):
+    q, k, v, g, b, st = inputs([4], 1, 1, 128, torch.bfloat16, gpu, seed=0)
+    with pytest.raises(RuntimeError):
+        delta_rule(q.cpu(), k.cpu(), v.cpu(), g.cpu(), b.cpu(), [4], st.cpu())
+    with pytest.raises(ValueError):
+        delta_rule(q, k, v, g, b, [3], st)
+    with pytest.raises(ValueError):
+        delta_rule(q.float(), k.float(), v.float(), g, b, [4], st)
