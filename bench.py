@@ -312,6 +312,7 @@ def bench_gdn(args):
     br_ms = _event_ms(lambda: delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, bst), args.steps)
     tokens = len(trow) + len(brow)
     flops = tokens * hv * 7 * d * d  # per token and head: decay, S^T k, the rank-1 write, S^T q
+    layer = _gdn_layer_times(args, w, hk, hv, d, dev)
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import deltanet as OD
@@ -343,8 +344,52 @@ def bench_gdn(args):
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
                      "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4),
                      "longest_run_tokens": max(tl), "us_per_token_longest_run": round(tr_ms * 1e3 / max(tl), 3)},
+        "layer": layer,
         "cpu_baseline": cpu,
     }), flush=True)
+
+
+def _gdn_layer_times(args, w, hk, hv, d, dev, hidden=2048, kernel=4):
+    """The whole DeltaNet layer (dan_amd.deltanet.DeltaNet: bf16 projections,
+    conv phase, delta rule, gated norm, output projection) over the same tree
+    with random weights, its layout built once per forward as dan shares it
+    across layers; and the conv phase kernel alone on the trunk phase, with
+    its algorithmic bytes (conv rows in and out, gate inputs and outputs)."""
+    import dataclasses
+    from types import SimpleNamespace
+
+    from dan_amd.attention import Batch
+    from dan_amd.deltanet import DeltaNet, RecurrentLayout, conv_phase
+
+    cfg = SimpleNamespace(linear_num_key_heads=hk, linear_num_value_heads=hv, linear_key_head_dim=d,
+                          linear_value_head_dim=d, linear_conv_kernel_dim=kernel, hidden_size=hidden,
+                          rms_norm_eps=1e-6)
+    torch.manual_seed(args.seed)
+    m = DeltaNet(cfg, 0).to(dev, torch.bfloat16)
+    c = m.conv_dim
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    segs = Batch(dataclasses.replace(
+        s, past={0: (torch.randn(kernel - 1, c, device=dev, generator=g).to(torch.bfloat16),
+                     torch.randn(hv, d, d, device=dev, generator=g) * 0.05)} if s.past else None,
+        saved={}, _mask=None) for s in w.segments)
+    n = w.num_tokens
+    x = torch.randn(n, hidden, device=dev, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            m(x, segs)
+        layer_ms = _event_ms(lambda: m(x, segs), args.steps)
+        qkv = torch.randn(n, c, device=dev, generator=g).to(torch.bfloat16)
+        ba = torch.randn(n, 2 * hv, device=dev, generator=g).to(torch.bfloat16)
+        hist = torch.cat([segs[i].past[0][0] for i in segs.recurrent.past_segments]) if segs.recurrent.past_segments else None
+        ph = segs.recurrent.trunk1
+        fn = lambda: conv_phase(qkv, hist, ph, m.conv1d.weight, ba[:, :hv], ba[:, hv:], m.A_log, m.dt_bias)
+        fn()
+        conv_ms = _event_ms(fn, args.steps)
+    t = len(ph.rows)
+    conv_bytes = (t * c * 2) * 2 + t * hv * (2 * 2 + 4 * 2)
+    return {"hidden": hidden, "conv_dim": c, "kernel": kernel, "layer_ms": round(layer_ms, 4),
+            "layer_tokens_per_s": round(n / layer_ms * 1e3, 1), "conv_phase_rows": t,
+            "conv_phase_ms": round(conv_ms, 4), "conv_phase_gbps_algorithmic": round(conv_bytes / conv_ms / 1e6, 1)}
 
 
 def bench_plan(args):

@@ -20,7 +20,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip")]
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip", "gdn_conv.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libdan_tree_attn.so")

@@ -116,7 +116,7 @@ class DanFp8QuantArgs(ctypes.Structure):
                 ("reserved", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
 
 
-GDN_ABI_VERSION = 1
+GDN_ABI_VERSION = 2
 
 
 class DanGdnArgs(ctypes.Structure):
@@ -130,10 +130,20 @@ class DanGdnArgs(ctypes.Structure):
                 ("workspace", _vp), ("workspace_bytes", _i64)]
 
 
+class DanGdnConvArgs(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("dtype", _i32), ("channels", _i32), ("kernel", _i32), ("num_rows", _i32),
+                ("num_hist_rows", _i32), ("num_ext", _i32), ("num_out", _i32),
+                ("src", _vp), ("src_stride", _i64), ("hist", _vp), ("ext", _vp), ("take", _vp), ("weight", _vp),
+                ("out", _vp), ("out_stride", _i64), ("num_heads", _i32), ("reserved", _i32), ("rows", _vp),
+                ("b", _vp), ("b_stride", _i64), ("a", _vp), ("a_stride", _i64), ("a_log", _vp), ("dt_bias", _vp),
+                ("beta", _vp), ("g", _vp)]
+
+
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
            "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
-           "dan_fp8_quantize", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version")
+           "dan_fp8_quantize", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version",
+           "dan_gdn_conv")
 
 _lock = threading.Lock()
 _lib = None
@@ -181,6 +191,8 @@ def load(path=LIB_PATH):
         lib.dan_gdn_fwd.restype = ctypes.c_int
         lib.dan_gdn_workspace_size.argtypes = [_i32, _i32]
         lib.dan_gdn_workspace_size.restype = _i64
+        lib.dan_gdn_conv.argtypes = [ctypes.POINTER(DanGdnConvArgs), _vp]
+        lib.dan_gdn_conv.restype = ctypes.c_int
         lib.dan_gdn_abi_version.argtypes = []
         lib.dan_gdn_abi_version.restype = ctypes.c_int
         got = (lib.dan_tree_attn_abi_version(), lib.dan_qkv_front_abi_version(), lib.dan_tree_attn_plan_abi_version(),
@@ -257,3 +269,11 @@ def gdn(args, stream, lib=None):
     rc = lib.dan_gdn_fwd(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_gdn_fwd failed ({rc}): {last_error(lib)}")
+
+
+def gdn_conv(args, stream, lib=None):
+    """Launch the conv and gates of one DeltaNet phase; raises RuntimeError with the library's message on failure."""
+    lib = lib or load()
+    rc = lib.dan_gdn_conv(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_gdn_conv failed ({rc}): {last_error(lib)}")

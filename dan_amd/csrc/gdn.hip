@@ -40,6 +40,7 @@ constexpr int kCols = 8;   // state columns per wave
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -112,22 +113,26 @@ __device__ inline float sum_rows8(float x) {
   return __builtin_bit_cast(float, (uint32_t)r32[0]) + __builtin_bit_cast(float, (uint32_t)r32[1]);
 }
 
-// One token's inputs, loaded ahead.
+// One token's inputs, loaded ahead: the lane's 16 rows of q and of k, and v.
 struct Slot {
-  u32x4 q0, q1, k0, k1;  // the lane's 16 rows of q and of k
-  float v, g, b, rq, rk;
+  u32x4 q0, q1, k0, k1;
+  float v;
 };
+
+__device__ inline float lane_value(float x, int j) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), j));
+}
 
 template <typename T>
 __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int unit = blockIdx.x * kWavesPerGroup + wave;  // (run, head, column block)
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  const int unit = blockIdx.x * kWavesPerGroup + wave;  // (run, head, column block), wave-uniform
   if (unit >= p.R * p.Hv * p.cblocks) return;           // whole waves only: no barrier follows
   const int cb = unit % p.cblocks, h = (unit / p.cblocks) % p.Hv, r = unit / (p.cblocks * p.Hv);
   const int hk = h / (p.Hv / p.Hk);
   const int re = lane >> 3, c = kCols * cb + (lane & 7);
-  const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r);
-  const int len = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1) - row0;
+  const int row0 = __builtin_amdgcn_readfirstlane(*(const DAN_GLOBAL int32_t *)(p.cu + r));
+  const int len = __builtin_amdgcn_readfirstlane(*(const DAN_GLOBAL int32_t *)(p.cu + r + 1)) - row0;
 
   // state rows 16 re .. 16 re + 15 of column c
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + c;
@@ -135,59 +140,63 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
 #pragma unroll
   for (int i = 0; i < 16; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(16 * re + i) * p.Dv);
 
-  const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh + 16 * re;
-  const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh + 16 * re;
-  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + c;
+  const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
+  const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
+  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh;
   auto load = [&](int t) __attribute__((always_inline)) {
     Slot sl;
     const int64_t row = row0 + t;
-    const DAN_GLOBAL u32x4 *qs = (const DAN_GLOBAL u32x4 *)(qh + row * p.q_st);
-    const DAN_GLOBAL u32x4 *ks = (const DAN_GLOBAL u32x4 *)(kh + row * p.k_st);
+    const DAN_GLOBAL u32x4 *qs = (const DAN_GLOBAL u32x4 *)(qh + row * p.q_st + 16 * re);
+    const DAN_GLOBAL u32x4 *ks = (const DAN_GLOBAL u32x4 *)(kh + row * p.k_st + 16 * re);
     sl.q0 = qs[0];
     sl.q1 = qs[1];
     sl.k0 = ks[0];
     sl.k1 = ks[1];
-    sl.v = (float)*(const DAN_GLOBAL T *)(vh + row * p.v_st);
-    sl.g = *(const DAN_GLOBAL float *)(p.g + row * p.Hv + h);
-    sl.b = *(const DAN_GLOBAL float *)(p.beta + row * p.Hv + h);
-    const DAN_GLOBAL float *nr = (const DAN_GLOBAL float *)(p.norms + (row * p.Hk + hk) * 2);
-    sl.rq = nr[0];
-    sl.rk = nr[1];
+    sl.v = (float)*(const DAN_GLOBAL T *)(vh + row * p.v_st + c);
     return sl;
+  };
+  // The scalars of 64 tokens from t0, one token per lane: g, beta, 1/|q|, 1/|k|.
+  auto load_gates = [&](int t0, f32x4 &gv) __attribute__((always_inline)) {
+    const int t = t0 + lane;
+    if (t < len) {
+      const int64_t row = row0 + t;
+      gv[0] = *(const DAN_GLOBAL float *)(p.g + row * p.Hv + h);
+      gv[1] = *(const DAN_GLOBAL float *)(p.beta + row * p.Hv + h);
+      const f32x2 nr = *(const DAN_GLOBAL f32x2 *)(p.norms + (row * p.Hk + hk) * 2);
+      gv[2] = nr[0];
+      gv[3] = nr[1];
+    }
   };
   T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + c;
   const float qscale = 0.08838834764831845f;  // Dk^-1/2 (dan/models/qwen3_5.py:110)
 
-  auto step = [&](int t, const Slot &sl) __attribute__((always_inline)) {
-    const f32x8 qa = cvt8<T>(sl.q0), qb = cvt8<T>(sl.q1), ka = cvt8<T>(sl.k0), kb = cvt8<T>(sl.k1);
-    float qv[16], kv[16];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qv[e] = (qa[e] * sl.rq) * qscale;
-      qv[8 + e] = (qb[e] * sl.rq) * qscale;
-      kv[e] = ka[e] * sl.rk;
-      kv[8 + e] = kb[e] * sl.rk;
-    }
-    const float a = expf(sl.g);
+  // The norm factors multiply the reduced sums, not the 32 elements:
+  // u = r_k (S^T k), the write is k (r_k w)^T, o = (r_q Dk^-1/2) (S^T q).
+  auto step = [&](int t, const Slot &sl, const f32x4 &gv) __attribute__((always_inline)) {
+    const int j = t & 63;
+    const float a = expf(lane_value(gv[0], j));
+    const float beta = lane_value(gv[1], j), rq = lane_value(gv[2], j), rk = lane_value(gv[3], j);
+    const f32x8 ka = cvt8<T>(sl.k0), kb = cvt8<T>(sl.k1);
     float u0 = 0.f, u1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       s[i] *= a;
       s[8 + i] *= a;
-      u0 = fmaf(kv[i], s[i], u0);
-      u1 = fmaf(kv[8 + i], s[8 + i], u1);
+      u0 = fmaf(ka[i], s[i], u0);
+      u1 = fmaf(kb[i], s[8 + i], u1);
     }
-    const float u = sum_rows8(u0 + u1);
-    const float w = sl.b * (sl.v - u);
+    const float u = sum_rows8(u0 + u1) * rk;
+    const float w = (beta * (sl.v - u)) * rk;
+    const f32x8 qa = cvt8<T>(sl.q0), qb = cvt8<T>(sl.q1);
     float o0 = 0.f, o1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      s[i] = fmaf(kv[i], w, s[i]);
-      s[8 + i] = fmaf(kv[8 + i], w, s[8 + i]);
-      o0 = fmaf(qv[i], s[i], o0);
-      o1 = fmaf(qv[8 + i], s[8 + i], o1);
+      s[i] = fmaf(ka[i], w, s[i]);
+      s[8 + i] = fmaf(kb[i], w, s[8 + i]);
+      o0 = fmaf(qa[i], s[i], o0);
+      o1 = fmaf(qb[i], s[8 + i], o1);
     }
-    const float o = sum_rows8(o0 + o1);
+    const float o = sum_rows8(o0 + o1) * (rq * qscale);
     if (re == 0) *(DAN_GLOBAL T *)(oh + (int64_t)(row0 + t) * p.o_st) = (T)o;
   };
 
@@ -195,13 +204,19 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
 #pragma unroll
   for (int j = 0; j < kAhead; ++j)
     if (j < len) f[j] = load(j);
-  for (int t = 0; t < len; t += kAhead) {
+  f32x4 gcur = {0.f, 0.f, 0.f, 0.f}, gnext = {0.f, 0.f, 0.f, 0.f};
+  load_gates(0, gcur);
+  if (64 < len) load_gates(64, gnext);
+  for (int t = 0; t < len; t += kAhead) {  // kAhead divides 64: a gate block starts at j = 0
+    if (t && (t & 63) == 0) {
+      gcur = gnext;
+      if (t + 64 < len) load_gates(t + 64, gnext);
+    }
 #pragma unroll
     for (int j = 0; j < kAhead; ++j) {
       if (t + j < len) {
-        const Slot cur = f[j];
+        step(t + j, f[j], gcur);
         if (t + j + kAhead < len) f[j] = load(t + j + kAhead);
-        step(t + j, cur);
       }
     }
   }

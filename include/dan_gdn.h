@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DAN_GDN_ABI_VERSION 1
+#define DAN_GDN_ABI_VERSION 2
 
 typedef struct {
   int32_t abi_version; /* DAN_GDN_ABI_VERSION */
@@ -61,6 +61,52 @@ typedef struct {
 int dan_gdn_fwd(const DanGdnArgs *args, void *stream);
 
 int64_t dan_gdn_workspace_size(int32_t num_tokens, int32_t num_k_heads);
+
+/* The input side of one DeltaNet phase, dan/models/qwen3_5.py:212-220
+ * (DeltaNet._phase up to the delta rule) with the gates of
+ * dan/fused.py:80-82 (delta_gates):
+ *   out[i] = silu(conv_i),  conv_i[c] = sum_j weight[c][j] * X(ext[take[i] + j])[c]
+ * over j < K, rounded to dtype before the silu (the reference's conv1d output),
+ *   beta[i][h] = sigmoid(b[rows[i]][h]) rounded to dtype, then widened to fp32
+ *   g[i][h] = -exp(a_log[h]) * softplus(a[rows[i]][h] + dt_bias[h])   (fp32)
+ * X(e) is a virtual source row: packed row e of src for e < N, zeros for
+ * e == N, hist row e - N - 1 above (the reference gathers from the same
+ * virtual source built with torch.cat, dan/models/qwen3_5.py:191-193; here
+ * the packed rows are read in place and only the cached histories are a
+ * separate buffer). Indices outside these ranges read as the zero row and a
+ * row index outside [0, N) gives beta = g = 0: the kernels never read out of
+ * bounds. */
+typedef struct {
+  int32_t abi_version;   /* DAN_GDN_ABI_VERSION */
+  int32_t dtype;         /* DanDtype of src, hist, weight, out, b and a: bf16 or f16 */
+  int32_t channels;      /* C, the conv width (2 Hk Dk + Hv Dv), a multiple of 8 */
+  int32_t kernel;        /* K, 2 to 4 */
+  int32_t num_rows;      /* N: packed rows */
+  int32_t num_hist_rows; /* rows of hist */
+  int32_t num_ext;       /* entries of ext */
+  int32_t num_out;       /* T: output rows */
+  const void *src; int64_t src_stride;  /* [N, C], row stride in elements (a column slice of the projection) */
+  const void *hist;                     /* [num_hist_rows, C] contiguous */
+  const int32_t *ext;                   /* [num_ext] virtual source rows */
+  const int32_t *take;                  /* [T] first ext entry of output row i's window */
+  const void *weight;                   /* [C, K] (nn.Conv1d's [C, 1, K]) */
+  void *out; int64_t out_stride;        /* [T, C] */
+  int32_t num_heads;                    /* Hv; 0 skips the gates */
+  int32_t reserved;
+  const int32_t *rows;                  /* [T] packed row of output row i */
+  const void *b; int64_t b_stride;      /* [N, Hv] */
+  const void *a; int64_t a_stride;      /* [N, Hv] */
+  const float *a_log;                   /* [Hv] */
+  const float *dt_bias;                 /* [Hv] */
+  float *beta;                          /* [T, Hv] */
+  float *g;                             /* [T, Hv] */
+} DanGdnConvArgs;
+
+/* Causal depthwise conv + silu over gathered windows, and the gates, for the
+ * rows of one phase. Replaces dan/models/qwen3_5.py:191-193 (the source
+ * concatenation), :216-218 (index_select, conv1d, silu, index_select) and
+ * the gathers of g and beta at :223, with dan/fused.py:80-82. */
+int dan_gdn_conv(const DanGdnConvArgs *args, void *stream);
 
 int dan_gdn_abi_version(void);
 

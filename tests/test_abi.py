@@ -54,6 +54,7 @@ STRUCTS = {
     "DanTreePlanArgs": _native.DanTreePlanArgs,
     "DanFp8QuantArgs": _native.DanFp8QuantArgs,
     "DanGdnArgs": _native.DanGdnArgs,
+    "DanGdnConvArgs": _native.DanGdnConvArgs,
 }
 
 
@@ -334,3 +335,31 @@ def test_gdn_argument_errors(lib, kw, status, needle):
 def test_gdn_no_runs_is_a_no_op(lib):
     assert lib.dan_gdn_fwd(ctypes.byref(_gdn_args(num_runs=0)), None) == _native.OK
     assert lib.dan_gdn_abi_version() == _native.GDN_ABI_VERSION
+
+
+def _conv_args(**kw):
+    a = _native.DanGdnConvArgs()
+    a.abi_version = _native.GDN_ABI_VERSION
+    a.dtype, a.channels, a.kernel, a.num_rows, a.num_ext, a.num_out = _native.DTYPE_BF16, 64, 4, 8, 11, 8
+    a.src_stride, a.out_stride = 64, 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(abi_version=1), _native.ERR_VERSION, "abi_version"),
+    (dict(dtype=_native.DTYPE_F32), _native.ERR_UNSUPPORTED, "dtype"),
+    (dict(kernel=5), _native.ERR_UNSUPPORTED, "kernel"),
+    (dict(channels=36), _native.ERR_UNSUPPORTED, "channels"),
+    (dict(num_ext=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
+    (dict(), _native.ERR_INVALID_ARGUMENT, "NULL"),
+])
+def test_gdn_conv_argument_errors(lib, kw, status, needle):
+    rc = lib.dan_gdn_conv(ctypes.byref(_conv_args(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_gdn_conv_no_rows_is_a_no_op(lib):
+    assert lib.dan_gdn_conv(ctypes.byref(_conv_args(num_out=0)), None) == _native.OK

@@ -1,0 +1,130 @@
+"""The gfx950 DeltaNet layer pieces against the oracle (oracle/deltanet.py,
+pinned by tests/test_deltanet_layer_oracle.py): the conv phase kernel
+(dan_gdn_conv: gathered causal conv + silu and the gates), and the whole
+layer (dan_amd.deltanet.DeltaNet) over a tree batch with a cached prefix, a
+save boundary and branches.
+
+Bars:
+- conv rows within one spacing of the model dtype (at most 2^-7 |ref| for
+  bf16, 2^-10 for fp16): the kernel rounds an fp32 sum where the oracle
+  rounds the float64 one, so only a value next to a rounding boundary can
+  differ, by one spacing, and silu then rounds again;
+- beta within one spacing of the model dtype; g within 2e-6 |g| + 1e-7;
+- the layer output within 2e-2 max|ref| and the saved state and conv tail
+  within 2e-2 of their largest magnitude: the layer's linears run in
+  hipBLASLt on the GPU and in fp32 on the CPU, which differ in the last bit
+  of their bf16 outputs, and the recurrence carries such differences on;
+- the layer over the tree equals the layer over each root-to-leaf path run
+  as its own sequence, on the GPU, within 1e-2 max|ref|."""
+import sys
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from dan_amd.deltanet import DeltaNet, RecurrentLayout, conv_phase
+from deltanet_cases import C, DK, DV, EPS, HIDDEN, HK, HV, KERNEL, path_batch, tree_batch, weights
+from oracle import deltanet as D
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def on(segs, dev):
+    for s in segs:
+        if s.past:
+            s.past = {k: tuple(t.to(dev) for t in v) for k, v in s.past.items()}
+    return segs
+
+
+def module(w, dev):
+    cfg = SimpleNamespace(linear_num_key_heads=HK, linear_num_value_heads=HV, linear_key_head_dim=DK,
+                          linear_value_head_dim=DV, linear_conv_kernel_dim=KERNEL, hidden_size=HIDDEN,
+                          rms_norm_eps=EPS)
+    m = DeltaNet(cfg, 0)
+    with torch.no_grad():
+        for name in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj"):
+            getattr(m, name).weight.copy_(w[name].float())
+        m.conv1d.weight.copy_(w["conv1d"].float())
+        m.dt_bias.copy_(w["dt_bias"].float())
+        m.A_log.copy_(w["A_log"].float())
+        m.norm.weight.copy_(w["norm"].float())
+    return m.to(dev, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_conv_phase_matches_oracle(gpu, dtype):
+    segs, _ = tree_batch(7)
+    n, k1 = sum(s.end - s.start for s in segs), KERNEL - 1
+    say(f"conv phase {dtype} N {n} C {C} K {KERNEL}")
+    g = torch.Generator().manual_seed(8)
+    proj = torch.randn(n, C + 64, generator=g).to(dtype)  # qkv as a column slice of a wider projection
+    hist = segs[0].past[0][0].to(dtype)
+    w = (torch.randn(C, 1, KERNEL, generator=g) * 0.5).to(dtype)
+    b = torch.randn(n, HV, generator=g).to(dtype) * 3
+    a = torch.randn(n, HV, generator=g).to(dtype) * 3
+    a[0, 0] = 30.0  # above softplus's threshold
+    a_log, dt_bias = torch.randn(HV, generator=g), torch.randn(HV, generator=g)
+    lay = RecurrentLayout.build(segs, k1, n, gpu)
+    vsrc = torch.cat([proj[:, :C], torch.zeros(1, C, dtype=dtype), hist]).double()
+    want = D.path_windows(segs, k1, n)
+    rb, rg = D.delta_gates(b, a, a_log, dt_bias)
+    spacing = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    pg = proj.to(gpu)
+    for ph in (lay.trunk1, lay.trunk2, lay.branches):
+        out, beta, gg = conv_phase(pg[:, :C], hist.to(gpu), ph, w.to(gpu), b.to(gpu), a.to(gpu), a_log.to(gpu),
+                                   dt_bias.to(gpu))
+        torch.cuda.synchronize()
+        rows = ph.rows.cpu().long()
+        ref = torch.stack([D.silu_conv(vsrc[want[int(r)][1]].to(dtype), w[:, 0]) [0] for r in rows])
+        e = (out.cpu().double() - ref.double()).abs()
+        say(f"  phase rows {len(rows)}: max |conv - ref| {e.max().item():.3e}")
+        assert (e <= spacing * ref.double().abs() + 1e-30).all()
+        eb = (beta.cpu() - rb[rows].float()).abs()
+        assert (eb <= spacing * rb[rows].float().abs()).all()
+        assert ((gg.cpu() - rg[rows]).abs() <= 2e-6 * rg[rows].abs() + 1e-7).all()
+
+
+def test_layer_matches_oracle(gpu):
+    w = weights(11)
+    segs, x = tree_batch(12)
+    say(f"DeltaNet layer bf16 N {x.shape[0]} Hk {HK} Hv {HV} Dv {DV}: tree with past, save and branches")
+    ref_y, _, ref_saved = D.deltanet_layer(w, x, segs, 0, HK, HV, DK, DV, KERNEL, EPS, recurrent=True)
+    gsegs, _ = tree_batch(12)
+    on(gsegs, gpu)
+    m = module(w, gpu)
+    with torch.no_grad():
+        y = m(x.to(gpu), gsegs)
+    torch.cuda.synchronize()
+    e = (y.cpu().float() - ref_y.float()).abs().max().item()
+    scale = ref_y.float().abs().max().item()
+    say(f"  max |y - ref| {e:.3e} (max |ref| {scale:.3e})")
+    assert e <= 2e-2 * scale
+    hist, state = gsegs[0].saved[0]
+    rh, rs = ref_saved[0]
+    es = (state.cpu() - rs).abs().max().item()
+    eh = (hist.cpu().float() - rh.float()).abs().max().item()
+    say(f"  saved state max diff {es:.3e}, conv tail {eh:.3e}")
+    assert es <= 2e-2 * rs.abs().max().item() and eh <= 2e-2 * rh.float().abs().max().item()
+
+
+def test_layer_tree_equals_paths(gpu):
+    w = weights(13)
+    segs, x = tree_batch(14)
+    on(segs, gpu)
+    psegs, px, paths = path_batch(segs, x)
+    say(f"DeltaNet layer: tree of {len(segs)} segments vs {len(paths)} root-to-leaf paths")
+    m = module(w, gpu)
+    with torch.no_grad():
+        y = m(x.to(gpu), segs).cpu().float()
+        py = m(px.to(gpu), psegs).cpu().float()
+    at, worst = 0, 0.0
+    for _, rows in paths:
+        worst = max(worst, (y[rows] - py[at:at + len(rows)]).abs().max().item())
+        at += len(rows)
+    say(f"  max |tree - paths| {worst:.3e}")
+    assert worst <= 1e-2 * py.abs().max().item()
