@@ -7,19 +7,23 @@
 //                     of q and of k (dan/models/qwen3_5.py:99-100), into the
 //                     caller's workspace -- the reductions leave the
 //                     sequential loop.
-//   gdn_kernel        one wave per (run, value head, block of 8 state columns);
-//                     lane 8 e + c owns rows 16 e .. 16 e + 15 of column c of
-//                     the state S [Dk = 128, Dv] (16 fp32 registers), so every
-//                     wave walks its run alone, without barriers. Per token,
-//                     with its inputs loaded four tokens ahead (the lane's 16
-//                     rows of q and k, v, g, beta and the two norm factors):
-//                       q' = (q r_q) Dk^-1/2, k' = k r_k      (fp32)
-//                       S <- exp(g) S;  u = S^T k' (two chains of 8 products,
-//                       then the eight row blocks summed by three VALU lane
-//                       exchanges, sum_rows8);  S <- S + k' (beta (v - u))^T;
-//                       o = S^T q' (likewise); row block 0 writes o.
-// The recurrence is sequential in the tokens of a run; its critical path per
-// token is one load-free chain of about 30 dependent operations.
+//   gdn_kernel        one wave per (run, value head, block of kCols = 8 state
+//                     columns); lane kCols e + c owns rows kRows e ..
+//                     kRows e + kRows - 1 (kRows = 16) of column c of the
+//                     state S [Dk = 128, Dv], in registers, so every wave
+//                     walks its run alone, without barriers. Per token:
+//                       S <- exp(g) S;  u = r_k (S^T k)  (two chains of
+//                       products, then the row blocks summed by VALU lane
+//                       exchanges, sum_column);  S <- S + k (r_k beta (v - u))^T;
+//                       o = (r_q Dk^-1/2) (S^T q); row block 0 writes o.
+//                     q, k and v are loaded kAhead = 8 tokens ahead into a
+//                     register FIFO, and g, beta and the norm factors once
+//                     per 64 tokens (one token per lane, read back with
+//                     readlane). All loads are unconditional (clamped to the
+//                     run), so the compiler's waits stay per slot instead of
+//                     draining every load in flight at each token.
+// The recurrence is sequential in the tokens of a run; a run's output and
+// final state do not depend on where a caller splits it into calls.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -35,8 +39,10 @@ namespace dan_gdn {
 
 constexpr int kDk = 128;
 constexpr int kWavesPerGroup = 4;
-constexpr int kAhead = 4;  // tokens loaded ahead (the FIFO depth)
-constexpr int kCols = 8;   // state columns per wave
+constexpr int kAhead = 8;  // tokens loaded ahead (the FIFO depth)
+constexpr int kCols = 8;                  // state columns per wave
+constexpr int kRows = kDk * kCols / 64;   // state rows per lane
+constexpr int kVecs = kRows / 8;          // 16-byte loads of q (and of k) per lane and token
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -99,10 +105,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_norms_kernel(const Pa
   if ((lane & 31) == 0) *(DAN_GLOBAL float *)(p.norms + item * 2 + (lane >> 5)) = 1.0f / sqrtf(ss + 1e-6f);
 }
 
-// Sum of x over the 8 lanes l with the same l % 8 (lanes l, l + 8, .., l + 56),
-// in every lane, on the VALU: a DPP rotation by 8 within each row of 16 lanes,
-// then the row swap (v_permlane16_swap) and the half swap (v_permlane32_swap).
-__device__ inline float sum_rows8(float x) {
+// Sum of x over the lanes l with the same l % kCols (one state column), in
+// every lane, on the VALU: DPP rotations within each row of 16 lanes (by 4
+// when four lanes of a row share a column, then by 8), then the row swap
+// (v_permlane16_swap) and the half swap (v_permlane32_swap).
+__device__ inline float sum_column(float x) {
+  if (kCols == 4)
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+                                                               0x124, 0xf, 0xf, false));
   x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
                                                              0x128, 0xf, 0xf, false));
   uint32_t u = __builtin_bit_cast(uint32_t, x);
@@ -113,9 +123,9 @@ __device__ inline float sum_rows8(float x) {
   return __builtin_bit_cast(float, (uint32_t)r32[0]) + __builtin_bit_cast(float, (uint32_t)r32[1]);
 }
 
-// One token's inputs, loaded ahead: the lane's 16 rows of q and of k, and v.
+// One token's inputs, loaded ahead: the lane's kRows rows of q and of k, and v.
 struct Slot {
-  u32x4 q0, q1, k0, k1;
+  u32x4 q[kVecs], k[kVecs];
   float v;
 };
 
@@ -130,15 +140,15 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
   if (unit >= p.R * p.Hv * p.cblocks) return;           // whole waves only: no barrier follows
   const int cb = unit % p.cblocks, h = (unit / p.cblocks) % p.Hv, r = unit / (p.cblocks * p.Hv);
   const int hk = h / (p.Hv / p.Hk);
-  const int re = lane >> 3, c = kCols * cb + (lane & 7);
+  const int re = lane / kCols, c = kCols * cb + lane % kCols;
   const int row0 = __builtin_amdgcn_readfirstlane(*(const DAN_GLOBAL int32_t *)(p.cu + r));
   const int len = __builtin_amdgcn_readfirstlane(*(const DAN_GLOBAL int32_t *)(p.cu + r + 1)) - row0;
 
-  // state rows 16 re .. 16 re + 15 of column c
+  // state rows kRows re .. kRows re + kRows - 1 of column c
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + c;
-  float s[16];
+  float s[kRows];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(16 * re + i) * p.Dv);
+  for (int i = 0; i < kRows; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(kRows * re + i) * p.Dv);
 
   const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
   const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
@@ -146,26 +156,25 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
   auto load = [&](int t) __attribute__((always_inline)) {
     Slot sl;
     const int64_t row = row0 + t;
-    const DAN_GLOBAL u32x4 *qs = (const DAN_GLOBAL u32x4 *)(qh + row * p.q_st + 16 * re);
-    const DAN_GLOBAL u32x4 *ks = (const DAN_GLOBAL u32x4 *)(kh + row * p.k_st + 16 * re);
-    sl.q0 = qs[0];
-    sl.q1 = qs[1];
-    sl.k0 = ks[0];
-    sl.k1 = ks[1];
+    const DAN_GLOBAL u32x4 *qs = (const DAN_GLOBAL u32x4 *)(qh + row * p.q_st + kRows * re);
+    const DAN_GLOBAL u32x4 *ks = (const DAN_GLOBAL u32x4 *)(kh + row * p.k_st + kRows * re);
+#pragma unroll
+    for (int m = 0; m < kVecs; ++m) {
+      sl.q[m] = qs[m];
+      sl.k[m] = ks[m];
+    }
     sl.v = (float)*(const DAN_GLOBAL T *)(vh + row * p.v_st + c);
     return sl;
   };
-  // The scalars of 64 tokens from t0, one token per lane: g, beta, 1/|q|, 1/|k|.
-  auto load_gates = [&](int t0, f32x4 &gv) __attribute__((always_inline)) {
-    const int t = t0 + lane;
-    if (t < len) {
-      const int64_t row = row0 + t;
-      gv[0] = *(const DAN_GLOBAL float *)(p.g + row * p.Hv + h);
-      gv[1] = *(const DAN_GLOBAL float *)(p.beta + row * p.Hv + h);
-      const f32x2 nr = *(const DAN_GLOBAL f32x2 *)(p.norms + (row * p.Hk + hk) * 2);
-      gv[2] = nr[0];
-      gv[3] = nr[1];
-    }
+  // The scalars of 64 tokens from t0, one token per lane (clamped to the
+  // run's last token): g, beta, 1/|q|, 1/|k|.
+  auto load_gates = [&](int t0, int last, f32x4 &gv) __attribute__((always_inline)) {
+    const int64_t row = row0 + min(t0 + lane, last);
+    gv[0] = *(const DAN_GLOBAL float *)(p.g + row * p.Hv + h);
+    gv[1] = *(const DAN_GLOBAL float *)(p.beta + row * p.Hv + h);
+    const f32x2 nr = *(const DAN_GLOBAL f32x2 *)(p.norms + (row * p.Hk + hk) * 2);
+    gv[2] = nr[0];
+    gv[3] = nr[1];
   };
   T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + c;
   const float qscale = 0.08838834764831845f;  // Dk^-1/2 (dan/models/qwen3_5.py:110)
@@ -176,52 +185,77 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
     const int j = t & 63;
     const float a = expf(lane_value(gv[0], j));
     const float beta = lane_value(gv[1], j), rq = lane_value(gv[2], j), rk = lane_value(gv[3], j);
-    const f32x8 ka = cvt8<T>(sl.k0), kb = cvt8<T>(sl.k1);
-    float u0 = 0.f, u1 = 0.f;
+    float kv[kRows], qv[kRows];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      s[i] *= a;
-      s[8 + i] *= a;
-      u0 = fmaf(ka[i], s[i], u0);
-      u1 = fmaf(kb[i], s[8 + i], u1);
+    for (int m = 0; m < kVecs; ++m) {
+      const f32x8 x = cvt8<T>(sl.k[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kv[8 * m + e] = x[e];
     }
-    const float u = sum_rows8(u0 + u1) * rk;
+    float u0 = 0.f, u1 = 0.f;  // two product chains
+#pragma unroll
+    for (int i = 0; i < kRows; i += 2) {
+      s[i] *= a;
+      s[i + 1] *= a;
+      u0 = fmaf(kv[i], s[i], u0);
+      u1 = fmaf(kv[i + 1], s[i + 1], u1);
+    }
+    const float u = sum_column(u0 + u1) * rk;
     const float w = (beta * (sl.v - u)) * rk;
-    const f32x8 qa = cvt8<T>(sl.q0), qb = cvt8<T>(sl.q1);
+#pragma unroll
+    for (int m = 0; m < kVecs; ++m) {
+      const f32x8 x = cvt8<T>(sl.q[m]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[8 * m + e] = x[e];
+    }
     float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      s[i] = fmaf(ka[i], w, s[i]);
-      s[8 + i] = fmaf(kb[i], w, s[8 + i]);
-      o0 = fmaf(qa[i], s[i], o0);
-      o1 = fmaf(qb[i], s[8 + i], o1);
+    for (int i = 0; i < kRows; i += 2) {
+      s[i] = fmaf(kv[i], w, s[i]);
+      s[i + 1] = fmaf(kv[i + 1], w, s[i + 1]);
+      o0 = fmaf(qv[i], s[i], o0);
+      o1 = fmaf(qv[i + 1], s[i + 1], o1);
     }
-    const float o = sum_rows8(o0 + o1) * (rq * qscale);
+    const float o = sum_column(o0 + o1) * (rq * qscale);
     if (re == 0) *(DAN_GLOBAL T *)(oh + (int64_t)(row0 + t) * p.o_st) = (T)o;
   };
 
-  Slot f[kAhead];
+  // Every load below is unconditional, with its token clamped to the run:
+  // loads under a branch make the compiler wait for all memory operations
+  // in flight at the join, which would serialize the loads ahead with the
+  // step. A full block of kAhead tokens needs no guard; the last tokens
+  // (fewer than kAhead) are the epilogue.
+  if (len > 0) {
+    const int last = len - 1;
+    Slot f[kAhead];
 #pragma unroll
-  for (int j = 0; j < kAhead; ++j)
-    if (j < len) f[j] = load(j);
-  f32x4 gcur = {0.f, 0.f, 0.f, 0.f}, gnext = {0.f, 0.f, 0.f, 0.f};
-  load_gates(0, gcur);
-  if (64 < len) load_gates(64, gnext);
-  for (int t = 0; t < len; t += kAhead) {  // kAhead divides 64: a gate block starts at j = 0
-    if (t && (t & 63) == 0) {
-      gcur = gnext;
-      if (t + 64 < len) load_gates(t + 64, gnext);
-    }
+    for (int j = 0; j < kAhead; ++j) f[j] = load(min(j, last));
+    f32x4 gcur = {0.f, 0.f, 0.f, 0.f}, gnext = {0.f, 0.f, 0.f, 0.f};
+    load_gates(0, last, gcur);
+    load_gates(64, last, gnext);
+    int t = 0;
+    for (;;) {  // blocks of 64 tokens, each with its gate vector
+      // gcur must be in registers before the token loop: a wait for it at the
+      // loop header would run on every iteration and drain the loads ahead.
+      asm volatile("" ::"v"(gcur[0]), "v"(gcur[1]), "v"(gcur[2]), "v"(gcur[3]));
+      int k = 0;
+      for (; k < 64 / kAhead && t + kAhead <= len; ++k, t += kAhead) {
 #pragma unroll
-    for (int j = 0; j < kAhead; ++j) {
-      if (t + j < len) {
-        step(t + j, f[j], gcur);
-        if (t + j + kAhead < len) f[j] = load(t + j + kAhead);
+        for (int j = 0; j < kAhead; ++j) {
+          step(t + j, f[j], gcur);
+          f[j] = load(min(t + j + kAhead, last));
+        }
       }
+      if (k < 64 / kAhead) break;  // fewer than kAhead tokens left, in gcur's block
+      gcur = gnext;
+      load_gates(t + 64, last, gnext);
     }
+#pragma unroll
+    for (int j = 0; j < kAhead - 1; ++j)
+      if (t + j < len) step(t + j, f[j], gcur);
   }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(16 * re + i) * p.Dv) = s[i];
+  for (int i = 0; i < kRows; ++i) *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(kRows * re + i) * p.Dv) = s[i];
 }
 
 }  // namespace dan_gdn
