@@ -11,7 +11,9 @@
 //                     row is loaded per output row and a full window only at a
 //                     run boundary. Sum in fp32 (j = 0 .. K-1, fused
 //                     multiply-adds), rounded to the I/O type as the
-//                     reference's conv1d output is, then silu in fp32.
+//                     reference's conv1d output is, then silu in fp32 (hardware
+//                     exp2 and reciprocal: the kernel is otherwise VALU-bound
+//                     on a full-precision exp and divide).
 //   gdn_gates_kernel  one thread per (output row, head): beta and g.
 // The packed projection rows are read in place through the virtual row index
 // (no concatenated copy of the source).
@@ -114,7 +116,9 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
 #pragma unroll
       for (int j = 1; j < K; ++j) acc = fmaf(w[j][c], x[j][c], acc);
       const float r = (float)(T)acc;  // the conv output in the I/O type
-      y[c] = r / (1.0f + expf(-r));
+      // silu(r) = r / (1 + e^-r) with the hardware exp2 and reciprocal (about
+      // one fp32 ulp each, far below the output type's spacing)
+      y[c] = r * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(r * -1.4426950408889634f));
     }
     *(DAN_GLOBAL u32x4 *)(static_cast<T *>(p.out) + (int64_t)i * p.out_stride + 8 * cg) = pack8<T>(y);
   }

@@ -102,3 +102,38 @@ def test_errors(gpu):
         delta_rule(q, k, v, g, b, [3], st)
     with pytest.raises(ValueError):
         delta_rule(q.float(), k.float(), v.float(), g, b, [4], st)
+
+
+def test_c3_tree_phases_match_oracle(gpu):
+    """The c3 tree at full size (5 trunks up to 1843 tokens, 45 branches,
+    8192 tokens, 16/16 heads of 128): the trunk phase from random states,
+    then the branch phase from the trunk finals, against the oracle's
+    float64 token recurrence on the same inputs, with the bf16 bars of the
+    small cases."""
+    from dan_amd import workloads
+
+    w = workloads.config3(0, device="cpu")
+    trunks = [(s.start, s.trunk) for s in w.segments]
+    branches = [(a, b - a, i) for i, s in enumerate(w.segments) for a, b in s.branches]
+    say(f"delta rule c3: {len(trunks)} trunks (longest {max(t for _, t in trunks)}), {len(branches)} branches")
+    g = torch.Generator().manual_seed(21)
+    n, h, d = w.num_tokens, 16, 128
+    q = torch.randn(n, h, d, generator=g).bfloat16()
+    k = torch.randn(n, h, d, generator=g).bfloat16()
+    v = torch.randn(n, h, d, generator=g).bfloat16()
+    gg = -(torch.rand(n, h, generator=g) * 0.1)
+    b = torch.rand(n, h, generator=g)
+    init = torch.randn(len(trunks), h, d, d, generator=g) * 0.05
+    trow = torch.cat([torch.arange(a, a + t) for a, t in trunks])
+    brow = torch.cat([torch.arange(a, a + m) for a, m, _ in branches])
+    bseg = torch.tensor([i for _, _, i in branches])
+    tl, bl = [t for _, t in trunks], [m for _, m, _ in branches]
+    dv = [x.to(gpu) for x in (q, k, v, gg, b)]
+    ot, ft = delta_rule(*(x[trow.to(gpu)] for x in dv), tl, init.to(gpu))
+    ob, fb = delta_rule(*(x[brow.to(gpu)] for x in dv), bl, ft.index_select(0, bseg.to(gpu)))
+    torch.cuda.synchronize()
+    torch.set_num_threads(8)
+    rt_o, rt_f = OD.delta_rule(*(x[trow] for x in (q, k, v, gg, b)), tl, init, recurrent=True)
+    check(ot, ft, rt_o, rt_f, torch.bfloat16)
+    rb_o, rb_f = OD.delta_rule(*(x[brow] for x in (q, k, v, gg, b)), bl, rt_f.index_select(0, bseg), recurrent=True)
+    check(ob, fb, rb_o, rb_f, torch.bfloat16)
