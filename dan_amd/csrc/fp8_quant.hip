@@ -116,6 +116,44 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(const Params p) {
   quantize_row<T>(row, p.xq + (int64_t)r * p.cols, p.cols, s);
 }
 
+// Rowwise, for rows of at most NC * 8 * kThreads values: the row stays in
+// registers between the amax and the quantization, so it is read from HBM
+// once and not again from L2. Loads are unconditional (clamped to the row's
+// last 8 values, then masked), so all NC are in flight together.
+template <typename T, int NC>
+__global__ __launch_bounds__(kThreads) void quant_rows_reg_kernel(const Params p) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
+  f32x8 x[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) x[j] = load8<T>(row + min(8 * (int)threadIdx.x + j * 8 * kThreads, p.cols - 8));
+  float a = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+    if (8 * (int)threadIdx.x + j * 8 * kThreads < p.cols) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(x[j][i]));
+    }
+  const float s = scale_of(block_amax(a, red));
+  if (threadIdx.x == 0) *(DAN_GLOBAL float *)(p.scale + r) = s;
+  uint8_t *out = p.xq + (int64_t)r * p.cols;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = 8 * threadIdx.x + j * 8 * kThreads;
+    if (c < p.cols) {
+      u32x2 q;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[j][4 * h] / s, x[j][4 * h + 1] / s, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(x[j][4 * h + 2] / s, x[j][4 * h + 3] / s, w, true);
+        q[h] = (uint32_t)w;
+      }
+      *(DAN_GLOBAL u32x2 *)(out + c) = q;
+    }
+  }
+}
+
 // Per tensor, step 1: zero the accumulator (scale[0] holds amax's bits until step 3).
 __global__ void zero_kernel(float *scale) { *(DAN_GLOBAL uint32_t *)scale = 0u; }
 
@@ -145,7 +183,12 @@ __global__ __launch_bounds__(kThreads) void quant_tensor_kernel(const Params p) 
 template <typename T>
 hipError_t launch(const Params &p, int mode, hipStream_t s) {
   if (mode == DAN_FP8_SCALE_ROW) {
-    hipLaunchKernelGGL(quant_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+    const int chunks = (p.cols + 8 * kThreads - 1) / (8 * kThreads);
+    if (chunks <= 1) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 1>), dim3(p.rows), dim3(kThreads), 0, s, p);
+    else if (chunks <= 2) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 2>), dim3(p.rows), dim3(kThreads), 0, s, p);
+    else if (chunks <= 4) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 4>), dim3(p.rows), dim3(kThreads), 0, s, p);
+    else if (chunks <= 8) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 8>), dim3(p.rows), dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(quant_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(1), 0, s, p.scale);
