@@ -102,7 +102,17 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
   const int head = isq ? hv : hv - p.H;
   const T *src = isq ? static_cast<const T *>(p.q) + t * p.q_st + head * p.q_sh
                      : static_cast<const T *>(p.k) + t * p.k_st + head * p.k_sh;
-  const f32x8 x = to_f32<T>(load16(src + 8 * j));
+  // Every operand is loaded here, unconditionally (a stand-in row, the lane's
+  // own x, where the norm weight or the rotary tables are unused): loads
+  // under branches would make the compiler wait for each one in turn.
+  const T *row = src + 8 * j;
+  const T *wrow = p.norm != DAN_FRONT_NORM_NONE ? static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j : row;
+  const int64_t cs_off = (int64_t)t * p.cs_st + min(8 * j, p.R - 8);
+  const T *crow = p.R > 0 ? static_cast<const T *>(p.cos) + cs_off : row;
+  const T *srow = p.R > 0 ? static_cast<const T *>(p.sin) + cs_off : row;
+  const u32x4 xraw = load16(row), wraw = load16(wrow), craw = load16(crow), sraw = load16(srow);
+  __builtin_amdgcn_sched_barrier(0);  // the scheduler would issue the weight load after the norm's math
+  const f32x8 x = to_f32<T>(xraw), w = to_f32<T>(wraw), cs = to_f32<T>(craw), sn = to_f32<T>(sraw);
 
   f32x8 n = x;
   if (p.norm != DAN_FRONT_NORM_NONE) {
@@ -112,7 +122,6 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
 #pragma unroll
     for (int m = 1; m < L; m <<= 1) ss += __shfl_xor(ss, m, L);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
-    const f32x8 w = to_f32<T>(load16(static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float y = x[i] * r;
@@ -132,8 +141,6 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
       pp[c] = (uint32_t)__shfl((int)word, partner, L);  // lane `partner` of this vector's L lanes
     }
     const f32x8 pv = to_f32<T>(pp);
-    const f32x8 cs = to_f32<T>(load16(static_cast<const T *>(p.cos) + t * p.cs_st + 8 * j));
-    const f32x8 sn = to_f32<T>(load16(static_cast<const T *>(p.sin) + t * p.cs_st + 8 * j));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float rot = j < half ? -pv[i] : pv[i];
