@@ -450,12 +450,16 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     if (kF8) pvs = *gbl(pd.v_scale);
   }
   // 8 values of key `key` (segment key coordinates) from d chunk c, as fp16.
+  // Branch-free: a key past the segment reads a stand-in row (the segment's
+  // first past or new row, which exists since the column block does) and is
+  // zeroed, so every thread's loads are in flight together (a load under a
+  // branch makes the compiler drain all loads at the join).
+  const TV *first = P > 0 ? pvp : vp + (int64_t)sg.start * p.v_st;
   auto row8 = [&](int key, int c) __attribute__((always_inline)) {
-    u32x4 x = {0, 0, 0, 0};
-    if (key < PN)
-      x = key < P ? load8_v<TV>(pvp + (int64_t)key * pv_st + 8 * c, pvs)
-                  : load8_v<TV>(vp + (int64_t)(sg.start + key - P) * p.v_st + 8 * c, vs);
-    return x;
+    const bool past = key < P, valid = key < PN;
+    const TV *src = !valid ? first : past ? pvp + (int64_t)key * pv_st : vp + (int64_t)(sg.start + key - P) * p.v_st;
+    const u32x4 x = load8_v<TV>(src + 8 * c, past ? pvs : vs);
+    return valid ? x : u32x4{0, 0, 0, 0};
   };
   const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;  // half-wave, lane in it
   const int c_lo = j >> 2, kp_lo = j & 3;
@@ -467,6 +471,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     r0[pass] = row8(key0 + 2 * kp, c);
     r1[pass] = row8(key0 + 2 * kp + 1, c);
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int pass = 0; pass < kPasses; ++pass) {
     const int item = hw + 8 * pass;
