@@ -9,9 +9,14 @@ Flags:
   -target-feature -packed-fp32-ops no packed fp32 VALU instructions.
   -amdgpu-mfma-vgpr-form           matrix-core results in VGPRs, so the softmax
                                    reads the score tile without AGPR copies.
-  -fno-honor-nans -mno-amdgpu-ieee v_max_f32 without a canonicalizing max in
-                                   front of every operand (the row max is the
-                                   softmax's largest VALU cost after exp).
+  -fno-honor-nans -mno-amdgpu-ieee tree_attn.hip only: v_max_f32 without a
+                                   canonicalizing max in front of every operand
+                                   (the attention's running-max raise). The
+                                   other sources keep IEEE NaN semantics, and
+                                   host-side argument checks read float bits.
+
+Each source compiles to its own object with its own flags; one link makes
+the library.
 """
 import os
 import shutil
@@ -21,16 +26,17 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip", "gdn_conv.hip")]
+# Extra flags per source (file name -> flags).
+SRC_FLAGS = {"tree_attn.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libdan_tree_attn.so")
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
-    "-fno-honor-nans", "-mno-amdgpu-ieee",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 
@@ -42,11 +48,7 @@ def hipcc():
     return path
 
 
-def build(out=OUT, extra=(), verbose=False):
-    """Compile the library; always recompiles. Returns the output path."""
-    os.makedirs(os.path.dirname(out), exist_ok=True)
-    tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-I", INCLUDE, *SRCS, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,6 +59,23 @@ def build(out=OUT, extra=(), verbose=False):
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{diag}")
     if diag.strip() and verbose:
         print(diag, file=sys.stderr)
+
+
+def build(out=OUT, extra=(), verbose=False):
+    """Compile the library; always recompiles. Returns the output path."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    obj_dir = os.path.join(os.path.dirname(out), "_obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, os.path.basename(src) + ".o") for src in SRCS]
+    cmds = [[hipcc(), *HIPCC_FLAGS, *SRC_FLAGS.get(os.path.basename(src), []), *extra, "-I", INCLUDE, "-c", src, "-o", obj]
+            for src, obj in zip(SRCS, objs)]
+    with ThreadPoolExecutor(max_workers=min(len(cmds), max(1, (os.cpu_count() or 1)))) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = out + ".tmp"
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

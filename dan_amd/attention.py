@@ -187,11 +187,15 @@ def _aligned(t):
 
 
 def _kernel_view(t):
-    """The tensor itself when the kernel can read it in place, else a
+    """The tensor itself when the kernel can read it in place, else a fresh
     contiguous copy (unaligned rows, or token strides too large for the
-    kernel's 32-bit in-tile offsets)."""
+    kernel's 32-bit in-tile offsets). The copy is a new allocation, so its
+    base is aligned; ``contiguous()`` would return a contiguous but
+    misaligned view unchanged."""
     small = abs(t.stride(-2)) * 64 < 2 ** 31
-    return t if _aligned(t) and small else t.contiguous()
+    if _aligned(t) and small:
+        return t
+    return torch.empty_like(t, memory_format=torch.contiguous_format).copy_(t)
 
 
 # Which tile planner builds a batch's tables: "device" (one upload and one

@@ -14,7 +14,8 @@
 // row, reduces |x| (wave shuffles, then LDS across the 4 waves), and on a
 // second pass over the row (now in L2) writes 8 codes per 8 values.
 // Per tensor: a zero fill, the same per-row amax folded into one fp32 by a
-// vector atomic max on its bits (non-negative floats order as integers),
+// vector atomic max on its bits (non-negative floats and NaN order as
+// integers),
 // the scale, then the quantizing pass with the one scale.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -57,30 +58,41 @@ __device__ inline f32x8 load8<float>(const float *p) {
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// max |x| over the work group, in every thread.
-__device__ inline float block_amax(float v, float *red) {
+// |x| as its fp32 bit pattern. Non-negative floats order as unsigned
+// integers and every NaN pattern lies above +inf's, so an integer max over
+// these propagates NaN as torch's amax does (dan/fused.py:88): a row holding
+// a NaN gets a NaN scale and NaN codes. (A float max would skip the NaN.)
+__device__ inline uint32_t abs_bits(float x) { return __builtin_bit_cast(uint32_t, x) & 0x7fffffffu; }
+
+// max |x| over the work group (as bits), in every thread.
+__device__ inline uint32_t block_amax(uint32_t v, uint32_t *red) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, m));
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = v;
   __syncthreads();
-  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  v = max(max(red[0], red[1]), max(red[2], red[3]));
   __syncthreads();  // red is reused by the next call
   return v;
 }
 
 template <typename T>
-__device__ inline float row_amax(const T *row, int cols) {
-  float a = 0.f;
+__device__ inline uint32_t row_amax(const T *row, int cols) {
+  uint32_t a = 0;
   for (int c = 8 * threadIdx.x; c < cols; c += 8 * kThreads) {
     const f32x8 x = load8<T>(row + c);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(x[i]));
+    for (int i = 0; i < 8; ++i) a = max(a, abs_bits(x[i]));
   }
   return a;
 }
 
-__device__ inline float scale_of(float amax) { return fmaxf(amax, 1e-12f) / kE4m3Max; }
+// max(amax, 1e-12) / 448 from amax's bits; a NaN amax gives a NaN scale
+// (torch's clamp keeps NaN).
+__device__ inline float scale_of(uint32_t amax_bits) {
+  const float amax = __builtin_bit_cast(float, amax_bits);
+  return amax_bits > 0x7f800000u ? amax : fmaxf(amax, 1e-12f) / kE4m3Max;
+}
 
 template <typename T>
 __device__ inline void quantize_row(const T *row, uint8_t *out, int cols, float scale) {
@@ -108,7 +120,7 @@ struct Params {
 // Rowwise: the row's scale, then its codes.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(const Params p) {
-  __shared__ float red[4];
+  __shared__ uint32_t red[4];
   const int r = blockIdx.x;
   const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
   const float s = scale_of(block_amax(row_amax<T>(row, p.cols), red));
@@ -122,18 +134,18 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(const Params p) {
 // last 8 values, then masked), so all NC are in flight together.
 template <typename T, int NC>
 __global__ __launch_bounds__(kThreads) void quant_rows_reg_kernel(const Params p) {
-  __shared__ float red[4];
+  __shared__ uint32_t red[4];
   const int r = blockIdx.x;
   const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
   f32x8 x[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) x[j] = load8<T>(row + min(8 * (int)threadIdx.x + j * 8 * kThreads, p.cols - 8));
-  float a = 0.f;
+  uint32_t a = 0;
 #pragma unroll
   for (int j = 0; j < NC; ++j)
     if (8 * (int)threadIdx.x + j * 8 * kThreads < p.cols) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(x[j][i]));
+      for (int i = 0; i < 8; ++i) a = max(a, abs_bits(x[j][i]));
     }
   const float s = scale_of(block_amax(a, red));
   if (threadIdx.x == 0) *(DAN_GLOBAL float *)(p.scale + r) = s;
@@ -160,16 +172,16 @@ __global__ void zero_kernel(float *scale) { *(DAN_GLOBAL uint32_t *)scale = 0u; 
 // Per tensor, step 2: each row's amax into the accumulator.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void amax_rows_kernel(const Params p) {
-  __shared__ float red[4];
+  __shared__ uint32_t red[4];
   const T *row = static_cast<const T *>(p.x) + (int64_t)blockIdx.x * p.x_stride;
-  const float a = block_amax(row_amax<T>(row, p.cols), red);
-  if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned int *>(p.scale), __float_as_uint(a));
+  const uint32_t a = block_amax(row_amax<T>(row, p.cols), red);
+  if (threadIdx.x == 0) atomicMax(reinterpret_cast<unsigned int *>(p.scale), a);
 }
 
 // Per tensor, step 3: amax -> scale.
 __global__ void finalize_kernel(float *scale) {
   DAN_GLOBAL float *s = (DAN_GLOBAL float *)scale;
-  *s = scale_of(__uint_as_float(*(DAN_GLOBAL uint32_t *)scale));
+  *s = scale_of(*(DAN_GLOBAL uint32_t *)scale);
 }
 
 // Per tensor, step 4: every row with the one scale.

@@ -30,6 +30,7 @@
 
 namespace dan {
 int fail(int status, const char *fmt, ...);  // tree_attn.hip: sets the thread's last-error message
+bool finite_nonnegative(float x);             // tree_attn.hip: decided from the float's bits
 extern thread_local char g_err[512];
 }  // namespace dan
 
@@ -197,8 +198,8 @@ int dan_qkv_front(const DanQkvFrontArgs *a, void *stream) {
   if (R < 0 || R > D || R % 16) return fail(DAN_ERR_INVALID_ARGUMENT, "rotary_dim %d must be a multiple of 16 in [0, %d]", R, D);
   if (a->norm < DAN_FRONT_NORM_NONE || a->norm > DAN_FRONT_NORM_RMS_ZERO_CENTERED)
     return fail(DAN_ERR_INVALID_ARGUMENT, "norm %d is not a DanFrontNorm", a->norm);
-  if (a->norm != DAN_FRONT_NORM_NONE && (!a->q_norm_weight || !a->k_norm_weight || !(a->eps >= 0.f)))
-    return fail(DAN_ERR_INVALID_ARGUMENT, "a norm needs q_norm_weight, k_norm_weight and eps >= 0");
+  if (a->norm != DAN_FRONT_NORM_NONE && (!a->q_norm_weight || !a->k_norm_weight || !dan::finite_nonnegative(a->eps)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "a norm needs q_norm_weight, k_norm_weight and a finite eps >= 0");
   if (a->num_saves < 0 || (a->num_saves > 0 && (!a->save_of || !a->saves || !a->v)))
     return fail(DAN_ERR_INVALID_ARGUMENT, "saves need save_of, saves and v");
   if (N == 0) return DAN_OK;

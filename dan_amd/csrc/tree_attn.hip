@@ -52,6 +52,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 
 #include "dan_tree_attn.h"
 
@@ -878,6 +879,20 @@ void tree_attn_kernel(const KParams args) {
 // ---------------------------------------------------------------- host side
 thread_local char g_err[512];
 
+// Argument checks on float values read their bits: the library's device code
+// is built with -fno-honor-nans, under which the compiler may fold a NaN
+// comparison (x != x, !(x > 0)) to a constant.
+bool finite_positive(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  return b != 0 && b < 0x7f800000u;  // +0, negatives (sign bit), inf and NaN fail
+}
+bool finite_nonnegative(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  return b < 0x7f800000u || b == 0x80000000u;  // +-0 or a finite positive
+}
+
 int fail(int status, const char *fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -959,13 +974,27 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   if (a->num_pasts > 0 && !a->pasts) return fail(DAN_ERR_INVALID_ARGUMENT, "num_pasts > 0 with NULL pasts");
   if (f8 && (!a->q_scale || !a->k_scale || !a->v_scale))
     return fail(DAN_ERR_INVALID_ARGUMENT, "e4m3 inputs need q_scale, k_scale and v_scale");
-  if (!(a->scale > 0.f) || !isfinite(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
+  if (!finite_positive(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
   if (a->phases < DAN_TREE_ATTN_PHASES_ALL || a->phases > DAN_TREE_ATTN_PHASE_ATTEND)
     return fail(DAN_ERR_INVALID_ARGUMENT, "phases %d: 0 (all), 1 (pack) or 2 (attend)", a->phases);
   const int64_t need = dan_tree_attn_workspace_size(Hkv, D, a->vt_cols);
   if (a->vt_cols <= 0 || need <= 0) return fail(DAN_ERR_INVALID_ARGUMENT, "vt_cols %d must be a positive multiple of %d", a->vt_cols, kKeyTile);
   if (!a->workspace || a->workspace_bytes < need || ((uintptr_t)a->workspace & 255))
     return fail(DAN_ERR_INVALID_ARGUMENT, "workspace needs %lld bytes, 256-byte aligned", (long long)need);
+  // Rows are read and written in 16-byte pieces: every row start must be
+  // 16-byte aligned (the wrapper passes a contiguous copy otherwise).
+  {
+    const int es_in = in == DAN_DTYPE_E4M3 ? 1 : 2, es_v = vd == DAN_DTYPE_F32 ? 4 : vd == DAN_DTYPE_E4M3 ? 1 : 2;
+    const int es_out = out == DAN_DTYPE_F32 ? 4 : 2;
+    const int64_t row_bytes[] = {a->q_stride_tok * es_in, a->q_stride_head * es_in, a->k_stride_tok * es_in,
+                                 a->k_stride_head * es_in, a->v_stride_tok * es_v, a->v_stride_head * es_v,
+                                 a->o_stride_tok * es_out, a->o_stride_head * es_out};
+    for (int64_t b : row_bytes)
+      if (b % 16) return fail(DAN_ERR_INVALID_ARGUMENT, "strides must keep rows 16-byte aligned");
+    const void *ptrs[] = {a->q, a->k, a->v, a->out};
+    for (const void *ptr : ptrs)
+      if ((uintptr_t)ptr & 15) return fail(DAN_ERR_INVALID_ARGUMENT, "q, k, v and out must be 16-byte aligned");
+  }
   // Per-lane offsets inside a tile are kept in 32 bits.
   if (a->k_stride_tok < 0 || a->k_stride_tok * kKeyTile >= (int64_t(1) << 31) || (int64_t)D * a->vt_cols >= (int64_t(1) << 31))
     return fail(DAN_ERR_UNSUPPORTED, "k token stride %lld or vt_cols %d is too large", (long long)a->k_stride_tok, a->vt_cols);

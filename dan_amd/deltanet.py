@@ -51,8 +51,9 @@ def delta_rule(q, k, v, g, beta, lengths, states, cu=None):
     if tuple(states.shape) != (r, hv, dk, dv):
         raise ValueError(f"states {tuple(states.shape)}: want {(r, hv, dk, dv)}")
     dev = q.device
-    q = q if _row_ok(q) else q.contiguous()
-    k = k if _row_ok(k) else k.contiguous()
+    # a fresh copy when rows are misaligned (contiguous() keeps a misaligned base)
+    q = q if _row_ok(q) else torch.empty_like(q, memory_format=torch.contiguous_format).copy_(q)
+    k = k if _row_ok(k) else torch.empty_like(k, memory_format=torch.contiguous_format).copy_(k)
     v = v if v.stride(-1) == 1 else v.contiguous()
     g = g.float().contiguous()
     beta = beta.float().contiguous()

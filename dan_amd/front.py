@@ -31,7 +31,10 @@ def _row_ok(t):
 
 
 def _view(t):
-    return t if _row_ok(t) else t.contiguous()
+    """t itself when its rows are 16-byte aligned, else a fresh contiguous copy
+    (a new allocation is aligned; ``contiguous()`` would return a contiguous
+    but misaligned tensor unchanged)."""
+    return t if _row_ok(t) else torch.empty_like(t, memory_format=torch.contiguous_format).copy_(t)
 
 
 def save_index(segments, num_tokens, device):

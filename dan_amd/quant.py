@@ -39,7 +39,7 @@ def fp8_quantize(x, fp8_max=E4M3_MAX, rowwise=True):
     m, k = x.shape
     es = x.element_size()
     if x.stride(1) != 1 or x.data_ptr() % 16 or (x.stride(0) * es) % 16 or x.stride(0) < k:
-        x = x.contiguous()
+        x = torch.empty_like(x, memory_format=torch.contiguous_format).copy_(x)  # a new, aligned allocation
     xq = torch.empty((m, k), dtype=E4M3, device=x.device)
     scale = torch.empty((m, 1) if rowwise else (1, 1), dtype=torch.float32, device=x.device)
     a = _native.DanFp8QuantArgs()

@@ -21,7 +21,12 @@
  *  - All tensors are device memory owned by the caller. The library borrows
  *    the pointers for one stream-ordered launch, allocates nothing and keeps
  *    nothing.
- *  - Strides are in elements. The head_dim axis must have unit stride.
+ *  - Strides are in elements. The head_dim axis must have unit stride, and
+ *    every row (token or head step of q, k, v, out and of each prefix-cache
+ *    entry) must start 16 bytes aligned: rows move in 16-byte pieces.
+ *  - Offsets inside a key tile are 32-bit: 64 * k_stride_tok * element size
+ *    of k and of every prefix-cache entry's k must stay below 2^31 bytes, and
+ *    so must head_dim * vt_cols * 2 (the V^T copy).
  *  - Every entry point returns 0 on success; on failure it returns a nonzero
  *    DanStatus and dan_tree_attn_last_error() describes the failure (a
  *    thread-local string, valid until the next call on the same thread).

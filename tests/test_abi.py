@@ -162,8 +162,15 @@ def test_bad_scale_dtype_and_workspace(lib):
     p = (ctypes.addressof(x) + 255) // 256 * 256
     full = dict(num_work=1, q=p, k=p, v=p, out=p, segments=p, work=p, key_lo=p, col_seg=p, vt_cols=64,
                 workspace=p, workspace_bytes=8 * 128 * 64 * 2)
-    assert lib.dan_tree_attn_fwd(ctypes.byref(_args(scale=0.0, **full)), None) == _native.ERR_INVALID_ARGUMENT
-    assert "scale" in _native.last_error(lib)
+    # non-positive, infinite and NaN scales (checked from the float's bits: the
+    # library is built with -fno-honor-nans, which may fold a NaN comparison)
+    for bad_scale in (0.0, -0.0, -1.0, float("inf"), float("nan"), -float("nan")):
+        assert lib.dan_tree_attn_fwd(ctypes.byref(_args(scale=bad_scale, **full)), None) == _native.ERR_INVALID_ARGUMENT
+        assert "scale" in _native.last_error(lib)
+    # 16-byte rows: misaligned pointers and strides are refused before launch
+    for mis in (dict(q=p + 2), dict(out=p + 8), dict(k_stride_tok=1028), dict(v_stride_head=4)):
+        assert lib.dan_tree_attn_fwd(ctypes.byref(_args(**dict(full, **mis))), None) == _native.ERR_INVALID_ARGUMENT
+        assert "16-byte" in _native.last_error(lib)
     small = dict(full, workspace_bytes=100)
     assert lib.dan_tree_attn_fwd(ctypes.byref(_args(**small)), None) == _native.ERR_INVALID_ARGUMENT
     assert "workspace" in _native.last_error(lib)
@@ -227,6 +234,11 @@ def test_front_checks_pointers_and_alignment(lib):
     assert "multiples of 8" in _native.last_error(lib)
     assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(full, cs_stride_tok=64))), None) == _native.ERR_INVALID_ARGUMENT
     assert "cs_stride_tok" in _native.last_error(lib)
+    # a norm with a NaN, infinite or negative eps is refused (decided from the float's bits)
+    normed = dict(full, norm=_native.FRONT_NORM_RMS, q_norm_weight=p, k_norm_weight=p)
+    for bad_eps in (float("nan"), float("inf"), -1e-6):
+        assert lib.dan_qkv_front(ctypes.byref(_front_args(**dict(normed, eps=bad_eps))), None) == _native.ERR_INVALID_ARGUMENT
+        assert "eps" in _native.last_error(lib)
 
 
 def test_plan_slots(lib):

@@ -63,6 +63,32 @@ def test_quantize_strided_rows_and_zero_rows(gpu):
     check_quant(big[::2, :64], False)
 
 
+def test_quantize_propagates_nan(gpu):
+    """A NaN in a row makes that row's scale NaN and all its codes NaN, as
+    dan's formula does on the CPU (torch's amax and clamp keep NaN,
+    dan/fused.py:88); per tensor, one NaN makes every code NaN. Other rows
+    keep the oracle's codes and scales bit for bit."""
+    say("fp8 quantize: NaN rows")
+    g = torch.Generator().manual_seed(11)
+    for dtype in (torch.bfloat16, torch.float32):
+        for k in (48, 4096, 20480):  # register-resident rows and the two-pass path
+            x = torch.randn(6, k, generator=g).to(dtype)
+            x[2, 5] = float("nan")
+            x[4, k - 1] = float("nan")
+            for rowwise in (True, False):
+                xq, s = DQ.fp8_quantize(x.to(gpu), rowwise=rowwise)
+                torch.cuda.synchronize()
+                rq, rs = OQ.fp8_quantize(x, rowwise)
+                got_nan = (xq.cpu().view(torch.uint8) & 0x7F) == 0x7F
+                want_nan = (rq.view(torch.uint8) & 0x7F) == 0x7F
+                assert torch.equal(got_nan, want_nan), (dtype, k, rowwise)
+                assert torch.equal(torch.isnan(s.cpu()), torch.isnan(rs))
+                ok = ~want_nan
+                assert torch.equal(xq.cpu().view(torch.uint8)[ok], rq.view(torch.uint8)[ok])
+                fin = ~torch.isnan(rs)
+                assert torch.equal(s.cpu()[fin], rs[fin])
+
+
 def test_fp8_linear_equals_dan_formulation_and_oracle(gpu):
     g = torch.Generator().manual_seed(3)
     for rowwise in (True, False):
