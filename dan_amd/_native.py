@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
 ABI_VERSION = 5
 KEY_TILE = 64
+SCRATCH_BYTES = 32 << 20  # DAN_TREE_ATTN_SCRATCH_BYTES: dan_tree_attn_fwd_noalloc's V^T scratch per GPU
 
 # DanStatus
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_VERSION = range(5)
@@ -139,7 +140,7 @@ class DanGdnConvArgs(ctypes.Structure):
                 ("beta", _vp), ("g", _vp)]
 
 
-EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
+EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_fwd_noalloc", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
            "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
            "dan_fp8_quantize", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version",
@@ -163,6 +164,8 @@ def load(path=LIB_PATH):
         lib = ctypes.CDLL(path, mode=ctypes.RTLD_LOCAL)
         lib.dan_tree_attn_fwd.argtypes = [ctypes.POINTER(DanTreeAttnArgs), _vp]
         lib.dan_tree_attn_fwd.restype = ctypes.c_int
+        lib.dan_tree_attn_fwd_noalloc.argtypes = [ctypes.POINTER(DanTreeAttnArgs), _vp]
+        lib.dan_tree_attn_fwd_noalloc.restype = ctypes.c_int
         lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
         lib.dan_tree_attn_tile_q.restype = ctypes.c_int
         lib.dan_tree_attn_head_groups.argtypes = [_i32, _i32]
@@ -232,6 +235,15 @@ def forward(args, stream, lib=None):
     rc = lib.dan_tree_attn_fwd(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_tree_attn_fwd failed (status {rc}): {last_error(lib)}")
+
+
+def forward_noalloc(args, stream, lib=None):
+    """Launch through dan_tree_attn_fwd_noalloc (the V^T copy in the library's
+    own scratch, nothing allocated); raises RuntimeError on failure."""
+    lib = lib or load()
+    rc = lib.dan_tree_attn_fwd_noalloc(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_tree_attn_fwd_noalloc failed (status {rc}): {last_error(lib)}")
 
 
 def front(args, stream, lib=None):

@@ -291,10 +291,12 @@ def _num_cus(device):
     return torch.cuda.get_device_properties(device).multi_processor_count
 
 
-def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL):
+def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL, noalloc=False):
     """The kernel call behind ``attend`` (no save side effect). ``phases``
     selects the launches (the C ABI's ``phases``): bench.py times the
-    attention launch alone with PHASE_ATTEND after a full call."""
+    attention launch alone with PHASE_ATTEND after a full call. ``noalloc``
+    launches through ``dan_tree_attn_fwd_noalloc`` (the V^T copy in the
+    library's own per-GPU scratch instead of a workspace)."""
     if not q.is_cuda:
         raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
                            f"{q.device} (the masked CPU path is the test oracle, not a backend)")
@@ -320,7 +322,7 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
     if plan.num_work:
         nbytes = _native.workspace_size(hkv, d, plan.vt_cols, lib)
-        ws = _workspace(plan, nbytes, q.device)
+        ws = None if noalloc else _workspace(plan, nbytes, q.device)
         a = _native.DanTreeAttnArgs()
         a.abi_version = _native.ABI_VERSION
         a.in_dtype = _DTYPES[qk_dtype]
@@ -339,11 +341,13 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
         a.tile_q = tile_q
         a.vt_cols = plan.vt_cols
         a.col_seg = plan.col_seg_d.data_ptr()
-        a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+        if ws is not None:
+            a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
         if q.dtype == E4M3:
             a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
         a.phases = phases
         units, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
         a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
-        _native.forward(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
+        launch = _native.forward_noalloc if noalloc else _native.forward
+        launch(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)

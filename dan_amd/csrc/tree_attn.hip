@@ -54,6 +54,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "dan_tree_attn.h"
 
 namespace dan {
@@ -905,6 +907,40 @@ int fail(int status, const char *fmt, ...) {
 // pair's group split over them.
 int heads_per_group(int rep) { return rep >= 3 ? 4 : rep; }
 
+// The V^T scratch of dan_tree_attn_fwd_noalloc: a device array in every GPU's
+// memory for the life of the process. In host code `scratch` names a host-side
+// stand-in, never the device memory: kernels get the per-device address that
+// hipGetSymbolAddress returns (scratch_address below).
+static __device__ __align__(256) uint8_t scratch[DAN_TREE_ATTN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device `stream` launches on, looked up once
+// per device with that device current. 0 on success.
+int scratch_address(hipStream_t stream, void **out) {
+  int dev = -1;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "cannot find the stream's device: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices) return fail(DAN_ERR_UNSUPPORTED, "device %d: the library serves devices 0..%d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if ((err = hipGetDevice(&cur)) != hipSuccess) return fail(DAN_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(err));
+    if (cur != dev && (err = hipSetDevice(dev)) != hipSuccess)
+      return fail(DAN_ERR_LAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(err));
+    void *ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess || !ptr)
+      return fail(DAN_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DAN_OK;
+}
+
 template <typename TV, int D>
 hipError_t launch_pack(const PackParams &pp, int blocks, hipStream_t stream) {
   hipLaunchKernelGGL((vt_pack_kernel<TV, D>), dim3(blocks), dim3(256), 0, stream, pp);
@@ -1044,6 +1080,24 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   else err = d128 ? launch_attn<_Float16, float, 128>(kp, grid, s) : launch_attn<_Float16, float, 64>(kp, grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
+}
+
+int dan_tree_attn_fwd_noalloc(const DanTreeAttnArgs *a, void *stream) {
+  using namespace dan;
+  g_err[0] = 0;
+  if (!a) return fail(DAN_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != DAN_TREE_ATTN_ABI_VERSION)
+    return fail(DAN_ERR_VERSION, "abi_version %d, library speaks %d", a->abi_version, DAN_TREE_ATTN_ABI_VERSION);
+  if (a->num_work == 0) return DAN_OK;
+  const int64_t need = dan_tree_attn_workspace_size(a->num_kv_heads, a->head_dim, a->vt_cols);
+  if (need > DAN_TREE_ATTN_SCRATCH_BYTES)
+    return fail(DAN_ERR_UNSUPPORTED, "the V^T copy needs %lld bytes; the library's scratch holds %lld (use dan_tree_attn_fwd "
+                "with a workspace)", (long long)need, (long long)DAN_TREE_ATTN_SCRATCH_BYTES);
+  DanTreeAttnArgs b = *a;
+  const int rc = scratch_address(static_cast<hipStream_t>(stream), &b.workspace);
+  if (rc != DAN_OK) return rc;
+  b.workspace_bytes = DAN_TREE_ATTN_SCRATCH_BYTES;
+  return dan_tree_attn_fwd(&b, stream);
 }
 
 }  // extern "C"

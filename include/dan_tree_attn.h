@@ -198,6 +198,23 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *args, void *stream);
 /* Bytes of workspace dan_tree_attn_fwd needs (0 for invalid arguments). */
 int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols);
 
+/* Capacity in bytes of the library's own V^T scratch (one per GPU). */
+#define DAN_TREE_ATTN_SCRATCH_BYTES (32LL << 20)
+
+/* dan_tree_attn_fwd without a workspace: the V^T copy goes to a scratch array
+ * the library keeps in each GPU's memory for the life of the process, and the
+ * call allocates nothing (no hipMalloc, no allocating library routine), so it
+ * can be made where allocation is not allowed: under HIP graph capture, in a
+ * fixed serving loop, or in a harness that forbids it. `workspace` and
+ * `workspace_bytes` of *args are ignored. It fails with
+ * DAN_ERR_UNSUPPORTED when dan_tree_attn_workspace_size() exceeds
+ * DAN_TREE_ATTN_SCRATCH_BYTES. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap in time on one GPU (different streams) race,
+ * and a DAN_TREE_ATTN_PHASE_ATTEND call reads what the last pack on that GPU
+ * left there. No counterpart in the reference (dan allocates through torch);
+ * it exists for callers that cannot allocate. */
+int dan_tree_attn_fwd_noalloc(const DanTreeAttnArgs *args, void *stream);
+
 /* Queries per work item the kernel expects for this head configuration
  * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172).
  * Returns 0 for an unsupported configuration. */

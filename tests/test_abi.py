@@ -67,6 +67,7 @@ def test_ctypes_layout_matches_header(tmp_path):
             lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
     lines.append(f'printf("ABI %d\\n", DAN_TREE_ATTN_ABI_VERSION);')
     lines.append(f'printf("KEY_TILE %d\\n", DAN_TREE_ATTN_KEY_TILE);')
+    lines.append('printf("SCRATCH %lld\\n", (long long)DAN_TREE_ATTN_SCRATCH_BYTES);')
     lines.append('printf("PHASES %d,%d,%d\\n", DAN_TREE_ATTN_PHASES_ALL, DAN_TREE_ATTN_PHASE_PACK, DAN_TREE_ATTN_PHASE_ATTEND);')
     lines.append('printf("FRONT %d,%d,%d,%d\\n", DAN_QKV_FRONT_ABI_VERSION, DAN_FRONT_NORM_NONE, DAN_FRONT_NORM_RMS, '
                  'DAN_FRONT_NORM_RMS_ZERO_CENTERED);')
@@ -88,6 +89,7 @@ def test_ctypes_layout_matches_header(tmp_path):
             assert int(got[f"{cname}.{fname}"]) == getattr(cls, fname).offset, f"{cname}.{fname}"
     assert int(got["ABI"]) == _native.ABI_VERSION
     assert int(got["KEY_TILE"]) == _native.KEY_TILE
+    assert int(got["SCRATCH"]) == _native.SCRATCH_BYTES
     assert got["PHASES"] == f"{_native.PHASES_ALL},{_native.PHASE_PACK},{_native.PHASE_ATTEND}"
     assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
                             f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
@@ -190,6 +192,19 @@ def test_bad_scale_dtype_and_workspace(lib):
         rc = lib.dan_tree_attn_fwd(ctypes.byref(_args(**dict(full, **sched))), None)
         assert rc == _native.ERR_INVALID_ARGUMENT
         assert "schedule" in _native.last_error(lib)
+
+
+def test_noalloc_checks_before_any_gpu_call(lib):
+    """dan_tree_attn_fwd_noalloc: NULL, version and a V^T copy larger than the
+    library's scratch come back as status codes without a GPU; no work is a
+    no-op."""
+    assert lib.dan_tree_attn_fwd_noalloc(None, None) == _native.ERR_INVALID_ARGUMENT
+    assert lib.dan_tree_attn_fwd_noalloc(ctypes.byref(_args(abi_version=3, num_work=1)), None) == _native.ERR_VERSION
+    assert lib.dan_tree_attn_fwd_noalloc(ctypes.byref(_args(num_work=0)), None) == _native.OK
+    cols = _native.SCRATCH_BYTES // (8 * 128 * 2) + 64  # one column block more than fits
+    big = _args(num_work=1, vt_cols=cols)
+    assert lib.dan_tree_attn_fwd_noalloc(ctypes.byref(big), None) == _native.ERR_UNSUPPORTED
+    assert "scratch" in _native.last_error(lib)
 
 
 def _front_args(**kw):
