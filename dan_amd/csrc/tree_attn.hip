@@ -9,8 +9,9 @@
 //
 // Two kernels run on the caller's stream:
 //   vt_pack_kernel     V (and each prefix-cache entry's v) -> fp16 V^T in the
-//                      caller's workspace, [Hkv][D][columns], one 64-aligned
-//                      column range per segment holding [past; new] keys.
+//                      caller's workspace, one 64-aligned column range per
+//                      segment holding [past; new] keys, each 64-key block
+//                      stored as the P V operand fragments (see Lds).
 //   tree_attn_kernel   the attention itself.
 //
 // Work decomposition of tree_attn_kernel
@@ -33,16 +34,18 @@
 //                                softmax state; row max/sum need one cross-half
 //                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max is not recomputed per tile, only raised when a tile's row sum shows
-//   that P left fp16's range (kSumLimit), so the O accumulators are rarely
-//   rescaled.
+//   max starts at the first tile's max and is not recomputed per tile, only
+//   raised when a tile's row sum shows that P left fp16's range (kSumLimit),
+//   so the O accumulators are rarely rescaled.
 //   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
 //                                B = P^T straight from the S^T registers: K rows
 //                                are staged in a permuted order that makes the
 //                                S^T accumulator layout the B-operand layout.
 // Staging: K and V^T tiles go from global memory straight into LDS
-// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep, into
-// rows padded by 16 bytes (conflict-free operand reads at constant offsets).
+// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep,
+// unpadded: K rows with XOR-swizzled 16-byte chunks, V^T as operand
+// fragments, both read without bank conflicts. One wave per SIMD issues all
+// of a tile's direct loads (kIssuers).
 // Pipelining: while the softmax of tile j runs on the VALU, the wave already
 // issues S = K Q^T of tile j+1 on the matrix core; the tile two ahead is in
 // flight from memory.
@@ -64,6 +67,14 @@ constexpr int kKeyTile = DAN_TREE_ATTN_KEY_TILE;  // keys per tile
 constexpr int kWaves = 8;                         // 2 per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWaveQ = 32;                        // queries per wave
+// Waves 0..kIssuers-1 (one per SIMD) issue every direct load of the stage
+// buffers; their SIMD partners only compute. The loads queue at the CU's
+// address unit; a queued wave cannot issue anything else, so the stall is
+// given to the wave that has slack (the older wave of each SIMD wins issue
+// arbitration and otherwise waits at the step barrier), and its partner runs
+// its S products alone meanwhile: the two waves of a SIMD settle half a phase
+// apart.
+constexpr int kIssuers = 4;
 constexpr float kSumLimit = 32768.0f;             // per-lane partial row sum of P: keeps p <= 2^15
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -261,6 +272,42 @@ __device__ inline void store4<float>(float *p, f32x4 x) {
   *gbl_mut(reinterpret_cast<f32x4 *>(p)) = x;
 }
 
+// Four output values of one register group, converted to the output type
+// and held as 32-bit words (2 for 16-bit outputs, 4 for fp32).
+template <typename TOut>
+struct Out4 {
+  static constexpr int kWords = (int)sizeof(TOut);
+  uint32_t w[kWords];
+};
+template <typename TOut>
+__device__ inline Out4<TOut> pack_out(const f32x16 &o, int first, float scale) {
+  const f32x4 x = {o[first] * scale, o[first + 1] * scale, o[first + 2] * scale, o[first + 3] * scale};
+  Out4<TOut> r;
+  if constexpr (std::is_same<TOut, float>::value) {
+    // (the whole vector is bit-cast: clang 22 bit-casts an ext_vector element
+    // by reading element 0)
+    const u32x4 u = __builtin_bit_cast(u32x4, x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.w[i] = u[i];
+  } else {
+    using V4 = TOut __attribute__((ext_vector_type(4)));
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_convertvector(x, V4));
+    r.w[0] = v[0];
+    r.w[1] = v[1];
+  }
+  return r;
+}
+// Eight consecutive output values (a then b) at p.
+template <typename TOut>
+__device__ inline void store8(TOut *p, const Out4<TOut> &a, const Out4<TOut> &b) {
+  if constexpr (std::is_same<TOut, float>::value) {
+    *gbl_mut(reinterpret_cast<u32x4 *>(p)) = u32x4{a.w[0], a.w[1], a.w[2], a.w[3]};
+    *gbl_mut(reinterpret_cast<u32x4 *>(p + 4)) = u32x4{b.w[0], b.w[1], b.w[2], b.w[3]};
+  } else {
+    *gbl_mut(reinterpret_cast<u32x4 *>(p)) = u32x4{a.w[0], a.w[1], b.w[0], b.w[1]};
+  }
+}
+
 template <typename TC>
 __device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
 template <>
@@ -388,35 +435,56 @@ __device__ inline const T *uniform_ptr(const T *p) {
   return (const T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
-// LDS layout of one of four stage buffers: K rows [64][D] (row m holds key
-// k_row(m)) then V^T rows [D][64], every row padded by one 16-byte chunk. A
-// buffer is a whole number of 1 KB direct-load blocks (K: 64 * (D/8 + 1)
-// chunks, V^T: D * 9 chunks); the pad chunks receive a duplicate of the row's
-// last chunk. A 1 KB sink after the buffers absorbs the direct-load slots that
-// round the per-wave load count up to a constant.
+// LDS layout of one of four stage buffers, without padding:
+//  - K rows [64][D] (row m holds key k_row(m)), each row's 16-byte chunks
+//    XOR-swizzled: chunk c of row m sits at slot c ^ kswz(m). The 16 lanes a
+//    ds_read_b128 serves together read one chunk of 16 consecutive rows, which
+//    the swizzle spreads over all 64 banks; the direct loads still move whole
+//    rows (1 KB = 64 lanes x 16 bytes of contiguous rows).
+//  - V^T as the P V operand fragments themselves: block (kj, db) holds, for
+//    lane l, d = 32 db + l % 32 and keys 16 kj + 8 (l / 32) .. + 8 (fp16), in
+//    lane order. The V^T copy in the workspace has the same order, so every
+//    direct load of V^T is 1 KB of contiguous memory and every operand read
+//    is 1 KB of contiguous LDS.
+// A 1 KB sink after the buffers absorbs the direct-load slots that round the
+// per-wave load count up to a constant (only when the blocks do not divide
+// evenly among the waves).
 template <int D, int KB = 2>  // KB: bytes per K element
 struct Lds {
-  static constexpr int kChunks = D * KB / 16 + 1;
-  static constexpr int kRow = kChunks * 16;
-  static constexpr int kBytes = kKeyTile * kRow;
-  static constexpr int kInsts = kKeyTile * kChunks / 64;
-  static constexpr int vChunks = kKeyTile / 8 + 1;
-  static constexpr int vRow = vChunks * 16;
-  static constexpr int vBytes = D * vRow;
-  static constexpr int vInsts = D * vChunks / 64;
-  static constexpr int slots = (kInsts + vInsts + kWaves - 1) / kWaves;  // direct loads per wave per tile
+  static constexpr int kRowBytes = D * KB;
+  static constexpr int kChunks = kRowBytes / 16;          // 16-byte chunks per K row
+  static constexpr int kBytes = kKeyTile * kRowBytes;
+  static constexpr int kBlocks = kBytes / 1024;
+  static constexpr int vBytes = D * kKeyTile * 2;         // fp16 V^T tile
+  static constexpr int vBlocks = vBytes / 1024;
+  static constexpr int blocks = kBlocks + vBlocks;
+  static constexpr int slots = (blocks + kIssuers - 1) / kIssuers;  // direct loads per issuing wave per tile
   static constexpr int buf = kBytes + vBytes;
   static constexpr int nbuf = 4;
   static constexpr int sink = nbuf * buf;
-  static constexpr int total = sink + 1024;
-  static_assert(kBytes == kInsts * 1024 && vBytes == vInsts * 1024, "whole 1 KB blocks");
+  static constexpr int total = sink + (blocks % kIssuers ? 1024 : 0);
+  // Swizzle: rows per 256-byte bank period, and the width of the chunk XOR.
+  static constexpr int kRowsPerPeriod = kRowBytes >= 256 ? 1 : 256 / kRowBytes;
+  static constexpr int kSwizzle = kChunks < 16 ? kChunks : 16;
+  static_assert(kBytes % 1024 == 0 && vBytes % 1024 == 0, "whole 1 KB blocks");
+  static_assert(total <= 160 * 1024, "LDS");
+  // Operand reads XOR the chunk into (buffer offset + lane offset): the
+  // buffer offsets must leave the lane offset's bits (32 rows) untouched.
+  static_assert(buf % (32 * kRowBytes) == 0, "buffer alignment");
 };
+
+// Slot of chunk c of K row m (see Lds).
+template <int D, int KB>
+__host__ __device__ constexpr int kswz(int m) {
+  return (m / Lds<D, KB>::kRowsPerPeriod) % Lds<D, KB>::kSwizzle;
+}
 
 // ---------------------------------------------------------------- V^T packing
 // One work group per (64-column block of the V^T copy, kv head): reads the 64
 // keys of the block (past rows from the segment's prefix-cache entry, new rows
 // from v; zero past the segment's end), converts them to fp16 and writes them
-// transposed, 128 contiguous bytes per d.
+// transposed, as the P V operand fragments of the block (16 KB contiguous per
+// block and kv head at D = 128; see Lds).
 // 8 consecutive values of v times `scale` (e4m3 only) -> 8 fp16 values.
 template <typename TV>
 __device__ inline u32x4 load8_v(const TV *p, float) {
@@ -487,11 +555,15 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     }
   }
   __syncthreads();
-  _Float16 *dst = p.vt + (int64_t)kvh * D * p.vt_cols + (int64_t)cb * kKeyTile;
+  // Out in operand-fragment order: chunk o = (kj * ND + db) * 64 + lane holds
+  // d = 32 db + lane % 32, keys 8 q .. 8 q + 7 with q = 2 kj + lane / 32.
+  constexpr int ND = D / 32;
+  _Float16 *dst = p.vt + ((int64_t)kvh * (p.vt_cols / kKeyTile) + cb) * (D * kKeyTile);
 #pragma unroll
-  for (int i = threadIdx.x; i < D * 8; i += 256) {
-    const int d = i >> 3, q = i & 7;  // row d, keys 8 q .. 8 q + 7
-    *gbl_mut(reinterpret_cast<u32x4 *>(dst + (int64_t)d * p.vt_cols + 8 * q)) =
+  for (int o = threadIdx.x; o < D * 8; o += 256) {
+    const int lane = o & 63, db = (o >> 6) % ND, kj = (o >> 6) / ND;
+    const int d = 32 * db + (lane & 31), q = 2 * kj + (lane >> 5);
+    *gbl_mut(reinterpret_cast<u32x4 *>(dst + 8 * o)) =
         *reinterpret_cast<const u32x4 *>(&tile[d * 32 + 4 * (q ^ ((d >> 3) & 7))]);
   }
 }
@@ -508,15 +580,22 @@ void tree_attn_kernel(const KParams args) {
   constexpr int KS = QK<TQK>::step;                   // k-step of Q K^T
   constexpr int NK = D / KS;                          // k-steps of Q K^T
   constexpr int CE = 16 / (int)sizeof(TQK);           // K / Q elements per 16-byte chunk
+  constexpr int CH = QK<TQK>::chunks;                 // 16-byte chunks per lane per k-step
   constexpr int ND = D / 32;   // 32-row d blocks of O^T
   constexpr int SLOTS = L::slots;
-  constexpr int KC = L::kChunks;
-  constexpr int VC = L::vChunks;
+  constexpr int NC = L::kChunks;
+  constexpr int RB = L::kRowBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, lq = lane & 31;
+  // LDS byte offsets of this lane's operand reads (see Lds). K: row lq of a
+  // 32-row block with its chunk swizzle and half-step folded in; the chunk
+  // of each k-step is XOR'd in per read (it only touches the low bits).
+  // V^T: the lane's 16 bytes of each operand fragment block.
+  const uint32_t k_lane = (uint32_t)(lq * RB + kswz<D, (int)sizeof(TQK)>(lq) * 16) ^ (uint32_t)(hl * CH * 16);
+  const uint32_t v_lane = (uint32_t)(L::kBytes + lane * 16);
 
   // units holds num_units records: clamping the range keeps a malformed
   // offset table from reading past it.
@@ -566,7 +645,8 @@ void tree_attn_kernel(const KParams args) {
       pk_st = pd.k_stride_tok;
       if (kF8) c_past = p.c * *gbl(p.q_scale) * *gbl(pd.k_scale);
     }
-    const _Float16 *vtp = p.vt + (int64_t)kvh * D * p.vt_cols + sg.vt_col;
+    // this segment's V^T column blocks (16 KB each at D = 128), tile j at vtp + j * D * 64
+    const _Float16 *vtp = p.vt + ((int64_t)kvh * (p.vt_cols / kKeyTile) + sg.vt_col / kKeyTile) * (D * kKeyTile);
 
     // Per-lane query state: lane owns query column lq of its wave. Padding
     // columns (past the tile, or an idle wave) read a clamped valid row and see
@@ -576,80 +656,57 @@ void tree_attn_kernel(const KParams args) {
     const int qrow = sg.start + min(ql, qend - 1);
     const int qk = qvalid ? P + ql : 0x3fffffff;
     Frag<TQK> qf[NK];  // loaded after the first tiles' direct loads are issued
-    // Raw score of the query against its own key (key coordinate P + query,
-    // token row qrow of k): the lane's half of the dot product plus lane ^ 32's.
-    auto self_score = [&](const Frag<TQK>(&q)[NK], int qr) __attribute__((always_inline)) {
-      const TQK *krow = kp + (int64_t)qr * p.k_st + KS / 2 * hl;
-      float acc = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) acc = dot_frag<TQK>(q[kk], load_frag<TQK>(krow + KS * kk), acc);
-      const LanePair lp = lane_pair(acc);
-      return lp.self + lp.other;
-    };
 
-    // Direct-load slots. A stage buffer is kInsts 1 KB blocks of K then vInsts
-    // of V^T; each wave issues SLOTS loads per tile: KF K blocks (wave + 8 s),
-    // VF V^T blocks, and one last slot that takes a leftover K or V^T block or
-    // goes to the sink. Per-lane element offsets from the tile's first row are
-    // loop-invariant; K keeps one per source layout (new tokens / past).
-    constexpr int KF = L::kInsts / kWaves, VF = L::vInsts / kWaves;
-    constexpr int KREM = L::kInsts - KF * kWaves, VREM = L::vInsts - VF * kWaves;
-    static_assert(SLOTS == KF + VF + 1 && KREM + VREM <= kWaves, "slot plan");
-    const int last_kind = wave < KREM ? 0 : wave < KREM + VREM ? 1 : 2;  // K, V^T, sink (wave-uniform)
-    const int last_blk = last_kind == 0 ? KF * kWaves + wave : last_kind == 1 ? L::kInsts + VF * kWaves + wave - KREM : 0;
+    // Direct-load slots. A stage buffer is kBlocks 1 KB blocks of K rows then
+    // vBlocks of V^T fragments; issuing wave w loads blocks w, w + kIssuers,
+    // ... (SLOTS per tile; a slot past the last block loads into the sink). K offsets are
+    // per source layout (new tokens / past) and include the row swizzle;
+    // V^T offsets are relative to the tile's 16 KB block of the copy.
     auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
-      const int pos = blk * 64 + lane;
-      return (uint32_t)((k_row(pos / KC) * st + CE * min(pos % KC, KC - 2)) * (int64_t)sizeof(TQK));
+      const int pos = blk * 64 + lane, m = pos / NC;
+      const int c = (pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m);
+      return (uint32_t)((k_row(m) * st + c * CE) * (int64_t)sizeof(TQK));
     };
-    auto v_offset = [&](int blk) __attribute__((always_inline)) {  // bytes; blk counts from the first V^T block
-      const int pos = blk * 64 + lane;
-      return (uint32_t)(((pos / VC) * p.vt_cols + 8 * min(pos % VC, VC - 2)) * 2);
-    };
-    uint32_t kon[KF > 0 ? KF : 1], kop[KF > 0 ? KF : 1], von[VF > 0 ? VF : 1];  // (KF is 0 for e4m3, D = 64)
+    uint32_t off_a[SLOTS], off_b[SLOTS];  // K: new / past offsets; V^T: offset in both
 #pragma unroll
-    for (int s = 0; s < KF; ++s) {
-      kon[s] = k_offset(wave + kWaves * s, p.k_st);
-      kop[s] = k_offset(wave + kWaves * s, pk_st);
+    for (int sl = 0; sl < SLOTS; ++sl) {
+      const int blk = wave + kIssuers * sl;
+      if (blk < L::kBlocks) {
+        off_a[sl] = k_offset(blk, p.k_st);
+        off_b[sl] = k_offset(blk, pk_st);
+      } else {
+        off_a[sl] = off_b[sl] = (uint32_t)((blk < L::blocks ? blk - L::kBlocks : 0) * 1024 + lane * 16);
+      }
     }
-#pragma unroll
-    for (int s = 0; s < VF; ++s) von[s] = v_offset(wave + kWaves * s);
-    // last slot: K offsets (new, past) or the V^T / sink offset
-    const uint32_t sink_off = (uint32_t)((lane & 7) * 16);  // sink: any valid V^T address (bytes)
-    const uint32_t lon = last_kind == 0 ? k_offset(last_blk, p.k_st) : last_kind == 1 ? v_offset(last_blk - L::kInsts) : sink_off;
-    const uint32_t lop = last_kind == 0 ? k_offset(last_blk, pk_st) : lon;
 
     // Issue the direct loads of key tile j into stage buffer b.
     auto issue = [&](int j, int b) __attribute__((always_inline)) {
       const int kb = j * kKeyTile;
       uint8_t *base = smem + b * L::buf;
-      const _Float16 *vtt = uniform_ptr(vtp + kb);
-      auto k_slow = [&](int blk) __attribute__((always_inline)) {  // tile straddles the past/new boundary or the segment's end
-        const int pos = blk * 64 + lane;
-        const int col = CE * min(pos % KC, KC - 2);
-        const int key = min(kb + k_row(pos / KC), PN - 1);
-        return key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col;
-      };
-      // (Separate loops per source layout: a select between two offset arrays
-      // would make the compiler keep them in scratch memory.)
-      if (kb + kKeyTile <= P) {  // wave-uniform tile base + per-lane 32-bit byte offsets
-        const TQK *tb = uniform_ptr(pkp + (int64_t)kb * pk_st);
+      const _Float16 *vtt = uniform_ptr(vtp + (int64_t)j * (D * kKeyTile));
+      const int ksrc = kb + kKeyTile <= P ? 0 : (kb >= P && kb + kKeyTile <= PN) ? 1 : 2;  // past, new, straddle
+      const TQK *tb = ksrc == 0 ? uniform_ptr(pkp + (int64_t)kb * pk_st) : uniform_ptr(kp + (int64_t)(sg.start + kb - P) * p.k_st);
 #pragma unroll
-        for (int s = 0; s < KF; ++s) dma16(tb, kop[s], base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) dma16(tb, lop, base + last_blk * 1024);
-      } else if (kb >= P && kb + kKeyTile <= PN) {
-        const TQK *tb = uniform_ptr(kp + (int64_t)(sg.start + kb - P) * p.k_st);
-#pragma unroll
-        for (int s = 0; s < KF; ++s) dma16(tb, kon[s], base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) dma16(tb, lon, base + last_blk * 1024);
-      } else {
-#pragma unroll
-        for (int s = 0; s < KF; ++s) dma16(k_slow(wave + kWaves * s), base + (wave + kWaves * s) * 1024);
-        if (last_kind == 0) dma16(k_slow(last_blk), base + last_blk * 1024);
+      for (int sl = 0; sl < SLOTS; ++sl) {
+        const int blk = wave + kIssuers * sl;  // wave-uniform
+        if (blk < L::kBlocks) {
+          if (ksrc == 0) {
+            dma16(tb, off_b[sl], base + blk * 1024);
+          } else if (ksrc == 1) {
+            dma16(tb, off_a[sl], base + blk * 1024);
+          } else {  // the tile straddles the past/new boundary or the segment's end
+            const int pos = blk * 64 + lane, m = pos / NC;
+            const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
+            const int key = min(kb + k_row(m), PN - 1);
+            dma16(key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col,
+                  base + blk * 1024);
+          }
+        } else if (blk < L::blocks) {
+          dma16(vtt, off_a[sl], base + blk * 1024);
+        } else {
+          dma16(vtt, off_a[sl], smem + L::sink);
+        }
       }
-#pragma unroll
-      for (int s = 0; s < VF; ++s) dma16(vtt, von[s], base + (L::kInsts + wave + kWaves * s) * 1024);
-      if (last_kind == 1) dma16(vtt, lon, base + last_blk * 1024);
-      if (last_kind == 2) dma16(vtt, lon, smem + L::sink);
     };
 
     f32x16 o[ND];
@@ -661,20 +718,25 @@ void tree_attn_kernel(const KParams args) {
 
     // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
     auto qk_phase = [&](int b, f32x16(&s)[2]) {
-      const uint8_t *kbuf = smem + b * L::buf;
+      // LDS address of this lane's row in buffer b. The dynamic LDS block is
+      // the kernel's only LDS object and starts at address 0, and buffer
+      // offsets are multiples of 32 rows, so XOR-ing a chunk into the address
+      // only changes the lane's row offset: one v_xor per k-step.
+      const uint32_t kbase = (uint32_t)(uintptr_t)(DAN_LDS uint8_t *)(smem + b * L::buf) + k_lane;
       s[0] = f32x16{};
       s[1] = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
+        Frag<TQK> a[2];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          Frag<TQK> a;
+        for (int i = 0; i < CH; ++i) {
+          const uint32_t off = kbase ^ (uint32_t)((2 * kk * CH + i) * 16);
 #pragma unroll
-          for (int i = 0; i < QK<TQK>::chunks; ++i)
-            a.c[i] = *reinterpret_cast<const u32x4 *>(kbuf + (32 * mb + lq) * L::kRow +
-                                                      ((2 * kk + hl) * QK<TQK>::chunks + i) * 16);
-          s[mb] = mfma_qk<TQK>(a, qf[kk], s[mb]);
+          for (int mb = 0; mb < 2; ++mb)
+            a[mb].c[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(off + mb * 32 * RB));
         }
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) s[mb] = mfma_qk<TQK>(a[mb], qf[kk], s[mb]);
       }
     };
     // Tree mask on boundary tiles. Key index of register r relative to the tile
@@ -782,12 +844,12 @@ void tree_attn_kernel(const KParams args) {
     };
     // O^T += V^T P^T over the 64 keys of stage buffer b.
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
-      const uint8_t *vbuf = smem + b * L::buf + L::kBytes;
+      const uint8_t *vbuf = smem + b * L::buf + v_lane;
 #pragma unroll
       for (int kj = 0; kj < 4; ++kj) {
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (32 * db + lq) * L::vRow + (2 * kj + hl) * 16);
+          const u32x4 a = *reinterpret_cast<const u32x4 *>(vbuf + (kj * ND + db) * 1024);
           o[db] = mfma32<_Float16>(a, pf[kj], o[db]);
         }
       }
@@ -796,31 +858,38 @@ void tree_attn_kernel(const KParams args) {
     const int ntile = w.ja1 + (w.jb1 - w.jb0);
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
-    // Prologue: tiles 0..2 in flight; meanwhile load q, key_lo and the
-    // query's own key. The running max m starts at the query's score against
-    // its own key (always visible to it). The compiler does not see the
-    // direct loads, so every load of its own is complete before they are
-    // issued: it waits for its loads by its own count, so a wait it placed
-    // for an earlier load would also drain the tiles in flight, and its
-    // waits for the loads below drain them anyway (tile 0 is needed next).
+    // Prologue: tiles 0..2 in flight; meanwhile load q and key_lo. The
+    // compiler does not see the direct loads, so every load of its own is
+    // complete before they are issued: it waits for its loads by its own
+    // count, so a wait it placed for an earlier load would also drain the
+    // tiles in flight, and its waits for the loads below drain them anyway
+    // (tile 0 is needed next).
     wait_vmem<0>();
 #pragma unroll
     for (int t = 0; t < 3; ++t)
-      if (t < ntile) issue(tile_of(t), t);
+      if (wave < kIssuers && t < ntile) issue(tile_of(t), t);
     qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
     {
       const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
     }
-    mneg = -self_score(qf, qrow) * c_new;
     wait_vmem<0>();
     barrier_lds();
     f32x16 sa[2], sb[2];
+    // The running max m starts at the largest visible score of the first
+    // tile (exact, so that tile's largest p is 1). A query that sees no key
+    // of the first tile (only when the segment has neither past nor trunk)
+    // starts from m = -3e38: its p stay 0 while its keys are hidden, and its
+    // first visible key overflows the tile's row sum, which raises m to that
+    // tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0). Finite
+    // throughout, so no inf - inf.
+    mneg = 3.0e38f;
     if (ntile > 0) {
       qk_phase(0, sa);
       mask_phase(tile_of(0), sa);
       fix_straddle(tile_of(0), sa);
+      mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
     }
 
     // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
@@ -832,14 +901,13 @@ void tree_attn_kernel(const KParams args) {
     auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
       const bool has_next = it + 1 < ntile;
       if (has_next) {
-        if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
-        else wait_vmem<0>();
+        if (wave < kIssuers) {
+          if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+          else wait_vmem<0>();
+        }
         barrier_lds();
-        // Waves 0-3 issue tile it+3's direct loads now, their SIMD partners
-        // (waves 4-7) after their softmax and S products below: the loads
-        // queue at the CU's address unit, and a wave waiting to issue them
-        // then has a partner that computes meanwhile.
-        if (wave < 4 && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+        // The issuing waves load tile it+3 now (see kIssuers).
+        if (wave < kIssuers && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
       }
       // S of the next tile is computed unconditionally (on the last tile it
       // reads a stale but complete buffer and is discarded) so that it shares a
@@ -848,7 +916,7 @@ void tree_attn_kernel(const KParams args) {
       const float ts = exp_phase(cur, c);
       qk_phase((it + 1) & 3, nxt);
       finish_tile(cur, ts, c);
-      if (wave >= 4 && has_next && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+
       pv_phase(it & 3);
       if (has_next) {
         mask_phase(tile_of(it + 1), nxt);
@@ -861,20 +929,24 @@ void tree_attn_kernel(const KParams args) {
       if (it < ntile) step(sb, sa);
     }
 
-    // Epilogue: O = O^T / l, written token-major [N, H, D].
+    // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
+    // r4 of block db holds d = 32 db + 8 r4 + 4 hl + (0..3); lanes l and
+    // l ^ 32 (the same query) trade halves so that each stores 8 contiguous
+    // d: lane hl = 0 the even groups, hl = 1 the odd ones.
     const float l = lsum + __shfl_xor(lsum, 32);
     const float linv = l > 0.f ? 1.0f / l : 0.f;
-    if (qvalid) {
-      TOut *row = static_cast<TOut *>(p.o) + (int64_t)(sg.start + ql) * p.o_st + (int64_t)head * p.o_sh + 4 * hl;
+    TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(sg.start + ql) * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
-      for (int db = 0; db < ND; ++db)
+    for (int db = 0; db < ND; ++db)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const f32x4 x = {o[db][4 * r4] * linv, o[db][4 * r4 + 1] * linv, o[db][4 * r4 + 2] * linv,
-                           o[db][4 * r4 + 3] * linv};
-          store4<TOut>(row + 32 * db + 8 * r4, x);
-        }
-    }
+      for (int jp = 0; jp < 2; ++jp) {
+        const Out4<TOut> e = pack_out<TOut>(o[db], 8 * jp, linv), od = pack_out<TOut>(o[db], 8 * jp + 4, linv);
+        const Out4<TOut> give = hl ? e : od, keep = hl ? od : e;
+        Out4<TOut> got;
+#pragma unroll
+        for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) got.w[w4] = __shfl_xor(give.w[w4], 32);
+        if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), hl ? got : keep, hl ? keep : got);
+      }
   }  // units
 }
 
