@@ -9,9 +9,8 @@
 //
 // Two kernels run on the caller's stream:
 //   vt_pack_kernel     V (and each prefix-cache entry's v) -> fp16 V^T in the
-//                      caller's workspace, one 64-aligned column range per
-//                      segment holding [past; new] keys, each 64-key block
-//                      stored as the P V operand fragments (see Lds).
+//                      caller's workspace, [Hkv][D][columns], one 64-aligned
+//                      column range per segment holding [past; new] keys.
 //   tree_attn_kernel   the attention itself.
 //
 // Work decomposition of tree_attn_kernel
@@ -34,18 +33,16 @@
 //                                softmax state; row max/sum need one cross-half
 //                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max starts at the first tile's max and is not recomputed per tile, only
-//   raised when a tile's row sum shows that P left fp16's range (kSumLimit),
-//   so the O accumulators are rarely rescaled.
+//   max is not recomputed per tile, only raised when a tile's row sum shows
+//   that P left fp16's range (kSumLimit), so the O accumulators are rarely
+//   rescaled.
 //   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
 //                                B = P^T straight from the S^T registers: K rows
 //                                are staged in a permuted order that makes the
 //                                S^T accumulator layout the B-operand layout.
 // Staging: K and V^T tiles go from global memory straight into LDS
-// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep,
-// unpadded: K rows with XOR-swizzled 16-byte chunks, V^T as operand
-// fragments, both read without bank conflicts. One wave per SIMD issues all
-// of a tile's direct loads (kIssuers).
+// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep, into
+// rows padded by 16 bytes (conflict-free operand reads at constant offsets).
 // Pipelining: while the softmax of tile j runs on the VALU, the wave already
 // issues S = K Q^T of tile j+1 on the matrix core; the tile two ahead is in
 // flight from memory.
@@ -184,6 +181,22 @@ __device__ inline T load_uniform(const T *p) {
     uint32_t w[sizeof(T) / 4];
   } raw;
   const DAN_GLOBAL uint32_t *src = gbl(reinterpret_cast<const uint32_t *>(p));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
+  return __builtin_bit_cast(T, raw);
+}
+
+// A small table entry every lane reads at the same address, read through the
+// constant address space: scalar loads (counted by lgkmcnt), so a wait for it
+// never drains the vector-memory loads in flight (the stage buffers' direct
+// loads). The entry must not change while the kernel runs.
+template <typename T>
+__device__ inline T load_scalar(const T *p) {
+  static_assert(sizeof(T) % 4 == 0, "table entries are dword multiples");
+  struct Raw {
+    uint32_t w[sizeof(T) / 4];
+  } raw;
+  const __attribute__((address_space(4))) uint32_t *src = (const __attribute__((address_space(4))) uint32_t *)p;
 #pragma unroll
   for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
   return __builtin_bit_cast(T, raw);
@@ -413,8 +426,13 @@ __device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // Uniform base address (an SGPR pair) plus a per-lane 32-bit byte offset:
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ inline void dma16(const void *base, uint32_t off, const uint8_t *lds) {
+// (The base is made visibly uniform here: it is uniform by construction, and
+// readfirstlane of a value the compiler already holds in SGPRs costs nothing.)
+__device__ inline void dma16(const void *base_any, uint32_t off, const uint8_t *lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(DAN_LDS const void *)lds;
+  const uint64_t bv = (uint64_t)(uintptr_t)base_any;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bv), hi = __builtin_amdgcn_readfirstlane((uint32_t)(bv >> 32));
+  const void *base = (const void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
                "s"(__builtin_amdgcn_readfirstlane(m0))
                : "memory", "m0");
@@ -426,6 +444,14 @@ __device__ inline void dma16(const void *addr, const uint8_t *lds) {
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// Wave-uniform integers, made visibly uniform (SGPRs).
+__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ inline int64_t uni64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)x),
+                 hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 // A wave-uniform pointer, made visibly uniform (SGPRs) for an "s" operand.
 template <typename T>
@@ -599,32 +625,188 @@ void tree_attn_kernel(const KParams args) {
 
   // units holds num_units records: clamping the range keeps a malformed
   // offset table from reading past it.
-  const int u_begin = max(*gbl(args.sched_off + blockIdx.x), 0);
-  const int u_end = min(*gbl(args.sched_off + blockIdx.x + 1), args.num_units);
+  const int u_begin = max(load_scalar(args.sched_off + blockIdx.x), 0);
+  const int u_end = min(load_scalar(args.sched_off + blockIdx.x + 1), args.num_units);
   // `args` is the first (and only) explicit kernel argument, at the start of
   // the kernarg segment. Each unit reads its fields through an opaque copy
   // of that address, so they are reloaded per unit (scalar loads) instead of
   // being hoisted out of the unit loop and held in SGPRs across the key
   // loop, where they would spill.
   const KArgPtr kseg = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+
+  // Where a unit's key tiles come from: its segment's new-token keys (kp, in
+  // packed rows from `start`), its prefix-cache keys (pkp), and its V^T
+  // column blocks (vtp; tile j at vtp + j * D * 64). Tiles are counted along
+  // the unit's visit order: [0, ja1) then [jb0, jb1).
+  struct Src {
+    const TQK *kp, *pkp;
+    const _Float16 *vtp;
+    int64_t pk_st;
+    int start, P, PN, ja1, jb0, ntile;
+  };
+  auto make_src = [&](const KParams &p, const DanUnit &un) __attribute__((always_inline)) {
+    const int kvh = un.group % p.num_kv_heads;
+    Src r;
+    r.kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
+    r.pkp = nullptr;
+    r.pk_st = 0;
+    if (un.past_len > 0) {
+      const DanPastDesc pd = load_scalar(p.pasts + un.past_idx);
+      r.pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
+      r.pk_st = pd.k_stride_tok;
+    }
+    r.vtp = p.vt + ((int64_t)kvh * (p.vt_cols / kKeyTile) + un.vt_col / kKeyTile) * (D * kKeyTile);
+    r.start = un.start;
+    r.P = un.past_len;
+    r.PN = un.past_len + un.n;
+    r.ja1 = un.item.ja1;
+    r.jb0 = un.item.jb0;
+    r.ntile = un.item.ja1 + (un.item.jb1 - un.item.jb0);
+    return r;
+  };
+  // A unit record is usable when its head group exists and it visits at
+  // least one key tile (every query sees its own key, so a planner never
+  // makes an empty item).
+  auto valid_unit = [&](const KParams &p, const DanUnit &un) __attribute__((always_inline)) {
+    return un.group >= 0 && un.group < p.num_kv_heads * p.chunks && un.item.ja1 >= 0 && un.item.jb1 >= un.item.jb0 &&
+           un.item.ja1 + (un.item.jb1 - un.item.jb0) > 0;
+  };
+
+  // Direct-load slots. A stage buffer is kBlocks 1 KB blocks of K rows then
+  // vBlocks of V^T fragments; wave w issues blocks w, w + 8, ... (SLOTS per
+  // tile; a slot past the last block loads into the sink). K offsets are per
+  // source layout (new tokens / past) and include the row swizzle; V^T
+  // offsets are relative to the tile's block of the copy.
+  auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
+    const int pos = blk * 64 + lane, m = pos / NC;
+    const int c = (pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m);
+    return (uint32_t)((k_row(m) * st + c * CE) * (int64_t)sizeof(TQK));
+  };
+  uint32_t off_a[SLOTS];  // K: new-token offsets; V^T and sink: offsets in the copy
+  {
+    const KParams &p = *(const KParams *)kseg;
+#pragma unroll
+    for (int sl = 0; sl < SLOTS; ++sl) {
+      const int blk = wave + kIssuers * sl;
+      off_a[sl] = blk < L::kBlocks ? k_offset(blk, p.k_st)
+                                   : (uint32_t)((blk < L::blocks ? blk - L::kBlocks : 0) * 1024 + lane * 16);
+    }
+  }
+  // K offsets for a prefix-cache layout of token stride st (zero elsewhere).
+  auto past_offsets = [&](int64_t st, uint32_t(&off)[SLOTS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int sl = 0; sl < SLOTS; ++sl) {
+      const int blk = wave + kIssuers * sl;
+      off[sl] = blk < L::kBlocks ? k_offset(blk, st) : 0u;
+    }
+  };
+
+  // Issue the direct loads of tile i (visit order) of source u into stage buffer b.
+  auto issue = [&](const KParams &p, const Src &u_any, const uint32_t(&off_b)[SLOTS], int i_any, int b_any)
+      __attribute__((always_inline)) {
+    // Every field is wave-uniform; saying so keeps the address arithmetic
+    // and the choice of source layout on the scalar unit (readfirstlane of a
+    // value already in SGPRs costs nothing).
+    const int i = uni(i_any), b = uni(b_any), P = uni(u_any.P), PN = uni(u_any.PN), start = uni(u_any.start);
+    const int ja1 = uni(u_any.ja1), jb0 = uni(u_any.jb0);
+    const TQK *ukp = uniform_ptr(u_any.kp), *upkp = uniform_ptr(u_any.pkp);
+    const int64_t pk_st = uni64(u_any.pk_st);
+    const int j = i < ja1 ? i : jb0 + (i - ja1);
+    const int kb = j * kKeyTile;
+    uint8_t *base = smem + b * L::buf;
+    const _Float16 *vtt = uniform_ptr(uniform_ptr(u_any.vtp) + (int64_t)j * (D * kKeyTile));
+    const int ksrc = kb + kKeyTile <= P ? 0 : (kb >= P && kb + kKeyTile <= PN) ? 1 : 2;  // past, new, straddle
+    const TQK *tb = ksrc == 0 ? uniform_ptr(upkp + (int64_t)kb * pk_st) : uniform_ptr(ukp + (int64_t)(start + kb - P) * p.k_st);
+    struct {
+      const TQK *kp, *pkp;
+      int64_t pk_st;
+      int start, P, PN;
+    } const u = {ukp, upkp, pk_st, start, P, PN};
+#pragma unroll
+    for (int sl = 0; sl < SLOTS; ++sl) {
+      const int blk = wave + kIssuers * sl;  // wave-uniform
+      if (blk < L::kBlocks) {
+        if (ksrc == 0) {
+          dma16(tb, off_b[sl], base + blk * 1024);
+        } else if (ksrc == 1) {
+          dma16(tb, off_a[sl], base + blk * 1024);
+        } else {  // the tile straddles the past/new boundary or the segment's end
+          const int pos = blk * 64 + lane, m = pos / NC;
+          const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
+          const int key = min(kb + k_row(m), u.PN - 1);
+          dma16(key < u.P ? u.pkp + (int64_t)key * u.pk_st + col : u.kp + (int64_t)(u.start + key - u.P) * p.k_st + col,
+                base + blk * 1024);
+        }
+      } else if (blk < L::blocks) {
+        dma16(vtt, off_a[sl], base + blk * 1024);
+      } else {
+        dma16(vtt, off_a[sl], smem + L::sink);
+      }
+    }
+  };
+
+  // The stage-buffer ring runs across units: the work group's k-th tile
+  // overall (in unit order) uses buffer k % 4. A unit's first three tiles
+  // are issued during the previous unit's last three steps, so the tile
+  // pipeline does not drain between units. `pre` counts the current unit's
+  // tiles the previous unit issued.
+  int gbase = 0, pre = 0;
+  // A wave's q fragments and key_lo for a unit: loaded in the unit's
+  // prologue, or, when the previous unit ran here, during that unit's last
+  // step (where they are no longer used), so the prologue does not wait a
+  // whole memory round trip for them.
+  Frag<TQK> qf[NK];
+  int qlo = 0;
+  bool q_ready = false;
+  auto load_q = [&](const KParams &p, const DanUnit &un) __attribute__((always_inline)) {
+    const int g = un.group, kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
+    const int hig = chunk * p.hpw + (wave % p.hpw), head = kvh * p.rep + hig;
+    const int qw0 = un.item.t0 + (wave / p.hpw) * kWaveQ, qend = un.item.t0 + un.item.tq;
+    const int ql = qw0 + lq;
+    const bool qvalid = hig < p.rep && qw0 < qend && ql < qend;
+    const int qrow = un.start + min(ql, qend - 1);
+    qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
+    const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st +
+                     (int64_t)min(head, p.num_kv_heads * p.rep - 1) * p.q_sh + KS / 2 * hl;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
+  };
   for (int u = u_begin; u < u_end; ++u) {
     KArgPtr kp_u = kseg;
     asm volatile("" : "+s"(kp_u));
     const KParams &p = *(const KParams *)kp_u;
-    const int groups = p.num_kv_heads * p.chunks;
-    const DanUnit un = load_uniform(p.units + u);  // one read resolves the unit
+    const DanUnit un = load_scalar(p.units + u);  // one read resolves the unit
+    if (!valid_unit(p, un)) {  // a malformed unit record: skip it (the previous unit prefetched nothing for it)
+      pre = 0;
+      continue;
+    }
     const int g = un.group;
-    if (g < 0 || g >= groups) continue;  // a malformed unit record: skip it
-    // Every wave is done with the previous unit's stage buffers before this
-    // unit's first tiles are loaded into them.
-    barrier_lds();
     const DanWorkItem &w = un.item;
     const int kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
-    struct {
-      int start, n, trunk, past_len, past_idx, vt_col;
-    } const sg = {un.start, un.n, un.trunk, un.past_len, un.past_idx, un.vt_col};
-    const int P = sg.past_len, PT = P + sg.trunk, PN = P + sg.n;
-    const int H = p.num_kv_heads * p.rep;
+    const Src cur = make_src(p, un);
+    const int P = cur.P, PT = P + un.trunk, ntile = cur.ntile;
+    uint32_t off_b[SLOTS];
+    past_offsets(cur.pk_st, off_b);
+    // The next unit, whose first tiles (nn of them) this unit's last steps
+    // prefetch. Only its tile count stays live; the few steps that issue its
+    // tiles re-read its record (scalar loads).
+    int nn = 0;
+    if (u + 1 < u_end) {
+      const DanUnit un2 = load_scalar(p.units + u + 1);
+      if (valid_unit(p, un2)) nn = min(un2.item.ja1 + (un2.item.jb1 - un2.item.jb0), 3);
+    }
+    // Tile i of the concatenation [this unit; the next unit's first nn tiles].
+    auto issue_cat = [&](int i) __attribute__((always_inline)) {
+      if (i < ntile) {
+        issue(p, cur, off_b, i, (gbase + i) & 3);
+      } else if (i - ntile < nn) {
+        const Src nxt = make_src(p, load_scalar(p.units + u + 1));
+        uint32_t off_nb[SLOTS];
+        past_offsets(nxt.pk_st, off_nb);
+        issue(p, nxt, off_nb, i - ntile, (gbase + i) & 3);
+      }
+    };
+    auto issued_cat = [&](int i) __attribute__((always_inline)) { return i < ntile + nn; };
 
     const int hig = chunk * p.hpw + (wave % p.hpw);
     const int head = kvh * p.rep + hig;
@@ -632,88 +814,26 @@ void tree_attn_kernel(const KParams args) {
     const int qend = w.t0 + w.tq;
     const bool wave_work = hig < p.rep && qw0 < qend;
 
-    const TQK *kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
-    const TQK *pkp = nullptr;
-    int64_t pk_st = 0;
     // Softmax exponent factor c of S: scale * log2(e), times q_scale * k_scale
     // for e4m3 (the prefix-cache entry's k has its own scale, c_past).
     float c_new = p.c, c_past = p.c;
-    if (kF8) c_new = c_past = p.c * *gbl(p.q_scale) * *gbl(p.k_scale);
-    if (P > 0) {
-      const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
-      pkp = static_cast<const TQK *>(pd.k) + (int64_t)kvh * pd.k_stride_head;
-      pk_st = pd.k_stride_tok;
-      if (kF8) c_past = p.c * *gbl(p.q_scale) * *gbl(pd.k_scale);
+    if (kF8) {
+      const float qs = load_scalar(p.q_scale);
+      c_new = c_past = p.c * qs * load_scalar(p.k_scale);
+      if (P > 0) c_past = p.c * qs * load_scalar(load_scalar(p.pasts + un.past_idx).k_scale);
     }
-    // this segment's V^T column blocks (16 KB each at D = 128), tile j at vtp + j * D * 64
-    const _Float16 *vtp = p.vt + ((int64_t)kvh * (p.vt_cols / kKeyTile) + sg.vt_col / kKeyTile) * (D * kKeyTile);
 
     // Per-lane query state: lane owns query column lq of its wave. Padding
     // columns (past the tile, or an idle wave) read a clamped valid row and see
     // every key, so they stay finite; they are never stored.
     const int ql = qw0 + lq;
     const bool qvalid = wave_work && ql < qend;
-    const int qrow = sg.start + min(ql, qend - 1);
     const int qk = qvalid ? P + ql : 0x3fffffff;
-    Frag<TQK> qf[NK];  // loaded after the first tiles' direct loads are issued
-
-    // Direct-load slots. A stage buffer is kBlocks 1 KB blocks of K rows then
-    // vBlocks of V^T fragments; issuing wave w loads blocks w, w + kIssuers,
-    // ... (SLOTS per tile; a slot past the last block loads into the sink). K offsets are
-    // per source layout (new tokens / past) and include the row swizzle;
-    // V^T offsets are relative to the tile's 16 KB block of the copy.
-    auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
-      const int pos = blk * 64 + lane, m = pos / NC;
-      const int c = (pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m);
-      return (uint32_t)((k_row(m) * st + c * CE) * (int64_t)sizeof(TQK));
-    };
-    uint32_t off_a[SLOTS], off_b[SLOTS];  // K: new / past offsets; V^T: offset in both
-#pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl) {
-      const int blk = wave + kIssuers * sl;
-      if (blk < L::kBlocks) {
-        off_a[sl] = k_offset(blk, p.k_st);
-        off_b[sl] = k_offset(blk, pk_st);
-      } else {
-        off_a[sl] = off_b[sl] = (uint32_t)((blk < L::blocks ? blk - L::kBlocks : 0) * 1024 + lane * 16);
-      }
-    }
-
-    // Issue the direct loads of key tile j into stage buffer b.
-    auto issue = [&](int j, int b) __attribute__((always_inline)) {
-      const int kb = j * kKeyTile;
-      uint8_t *base = smem + b * L::buf;
-      const _Float16 *vtt = uniform_ptr(vtp + (int64_t)j * (D * kKeyTile));
-      const int ksrc = kb + kKeyTile <= P ? 0 : (kb >= P && kb + kKeyTile <= PN) ? 1 : 2;  // past, new, straddle
-      const TQK *tb = ksrc == 0 ? uniform_ptr(pkp + (int64_t)kb * pk_st) : uniform_ptr(kp + (int64_t)(sg.start + kb - P) * p.k_st);
-#pragma unroll
-      for (int sl = 0; sl < SLOTS; ++sl) {
-        const int blk = wave + kIssuers * sl;  // wave-uniform
-        if (blk < L::kBlocks) {
-          if (ksrc == 0) {
-            dma16(tb, off_b[sl], base + blk * 1024);
-          } else if (ksrc == 1) {
-            dma16(tb, off_a[sl], base + blk * 1024);
-          } else {  // the tile straddles the past/new boundary or the segment's end
-            const int pos = blk * 64 + lane, m = pos / NC;
-            const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
-            const int key = min(kb + k_row(m), PN - 1);
-            dma16(key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(sg.start + key - P) * p.k_st + col,
-                  base + blk * 1024);
-          }
-        } else if (blk < L::blocks) {
-          dma16(vtt, off_a[sl], base + blk * 1024);
-        } else {
-          dma16(vtt, off_a[sl], smem + L::sink);
-        }
-      }
-    };
 
     f32x16 o[ND];
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
     float mneg, lsum = 0.f;  // exponent offset -m of the running max m
-    int qlo;
     u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
     // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
@@ -787,12 +907,11 @@ void tree_attn_kernel(const KParams args) {
     // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
     // partial row sum of the fp16-rounded values that P V uses (exact products,
     // fp32 accumulation), so rounding P mostly cancels in O / l. The running
-    // max m starts at tile 0's max and is not recomputed per tile: a partial
-    // row sum above kSumLimit (or inf) means some p left fp16's range or m is
-    // stale by more than log2(kSumLimit / 32); only then is m raised to the
-    // tile's max (O and l rescaled) and the tile's P redone. A lane holds half
-    // of its query's keys and the other half sits in lane ^ 32; both keep the
-    // same m.
+    // max m is not recomputed per tile: a partial row sum above kSumLimit (or
+    // inf) means some p left fp16's range or m is stale by more than
+    // log2(kSumLimit / 32); only then is m raised to the tile's max (O and l
+    // rescaled) and the tile's P redone. A lane holds half of its query's keys
+    // and the other half sits in lane ^ 32; both keep the same m.
     auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
       float m8[8];
 #pragma unroll
@@ -855,25 +974,22 @@ void tree_attn_kernel(const KParams args) {
       }
     };
 
-    const int ntile = w.ja1 + (w.jb1 - w.jb0);
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
-    // Prologue: tiles 0..2 in flight; meanwhile load q and key_lo. The
-    // compiler does not see the direct loads, so every load of its own is
-    // complete before they are issued: it waits for its loads by its own
-    // count, so a wait it placed for an earlier load would also drain the
-    // tiles in flight, and its waits for the loads below drain them anyway
-    // (tile 0 is needed next).
-    wait_vmem<0>();
+    // Prologue: the tiles 0..2 the previous unit did not prefetch, and the
+    // next unit's tiles that fall within three of this unit's start (when this
+    // unit is shorter than three tiles), then q and key_lo. The buffers they
+    // go to held tiles that every wave finished before the previous unit's
+    // last barrier. Waiting for q (a load the compiler sees, issued last)
+    // also completes every direct load issued before it.
+    if (wave < kIssuers) {
 #pragma unroll
-    for (int t = 0; t < 3; ++t)
-      if (wave < kIssuers && t < ntile) issue(tile_of(t), t);
-    qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
-    {
-      const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st + (int64_t)min(head, H - 1) * p.q_sh + KS / 2 * hl;
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
+      for (int t = 0; t < 3; ++t)
+        if (t >= pre && t < ntile) issue(p, cur, off_b, t, (gbase + t) & 3);
+      for (int t = ntile; t < 3; ++t) issue_cat(t);
     }
+    if (!q_ready) load_q(p, un);
+    q_ready = false;
     wait_vmem<0>();
     barrier_lds();
     f32x16 sa[2], sb[2];
@@ -884,50 +1000,55 @@ void tree_attn_kernel(const KParams args) {
     // first visible key overflows the tile's row sum, which raises m to that
     // tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0). Finite
     // throughout, so no inf - inf.
-    mneg = 3.0e38f;
-    if (ntile > 0) {
-      qk_phase(0, sa);
-      mask_phase(tile_of(0), sa);
-      fix_straddle(tile_of(0), sa);
-      mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
-    }
+    qk_phase(gbase & 3, sa);
+    mask_phase(tile_of(0), sa);
+    fix_straddle(tile_of(0), sa);
+    mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
 
     // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
-    // core, then O += V P of tile it while the VALU masks S(it+1).
-    // Stage buffer of tile t is t % 4: when tile it+3 is issued (after the
-    // barrier of step it), its buffer's previous tile it-1 is finished by every
-    // wave.
+    // core, then O += V P of tile it while the VALU masks S(it+1). The last
+    // step of the unit has no next tile. Every step starts with a barrier,
+    // after which tile it+3 of the concatenation (this unit, then the next
+    // unit's first tiles) is issued into the buffer that tile it-1 used:
+    // every wave has finished tile it-1 before the barrier.
     int it = 0;
-    auto step = [&](f32x16(&cur)[2], f32x16(&nxt)[2]) {
-      const bool has_next = it + 1 < ntile;
-      if (has_next) {
-        if (wave < kIssuers) {
-          if (it + 2 < ntile) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
-          else wait_vmem<0>();
-        }
-        barrier_lds();
-        // The issuing waves load tile it+3 now (see kIssuers).
-        if (wave < kIssuers && it + 3 < ntile) issue(tile_of(it + 3), (it + 3) & 3);
+    auto step = [&](auto last, f32x16(&cur_s)[2], f32x16(&nxt_s)[2]) {
+      constexpr bool kLast = decltype(last)::value;
+      if (!kLast && wave < kIssuers) {
+        if (issued_cat(it + 2)) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+        else wait_vmem<0>();
       }
-      // S of the next tile is computed unconditionally (on the last tile it
-      // reads a stale but complete buffer and is discarded) so that it shares a
-      // basic block with the softmax VALU work and the two interleave.
+      barrier_lds();
+      // The issuing waves load tile it+3 now (see kIssuers).
+      if (wave < kIssuers) issue_cat(it + 3);
+      if (kLast && nn > 0) {  // q and key_lo of the next unit (this unit's are no longer used)
+        load_q(p, load_scalar(p.units + u + 1));
+        q_ready = true;
+      }
       const float c = tile_c(tile_of(it));
-      const float ts = exp_phase(cur, c);
-      qk_phase((it + 1) & 3, nxt);
-      finish_tile(cur, ts, c);
-
-      pv_phase(it & 3);
-      if (has_next) {
-        mask_phase(tile_of(it + 1), nxt);
-        fix_straddle(tile_of(it + 1), nxt);
+      const float ts = exp_phase(cur_s, c);
+      if (!kLast) qk_phase((gbase + it + 1) & 3, nxt_s);
+      finish_tile(cur_s, ts, c);
+      pv_phase((gbase + it) & 3);
+      if (!kLast) {
+        mask_phase(tile_of(it + 1), nxt_s);
+        fix_straddle(tile_of(it + 1), nxt_s);
       }
       ++it;
     };
-    while (it < ntile) {
-      step(sa, sb);
-      if (it < ntile) step(sb, sa);
+    using NotLast = std::integral_constant<bool, false>;
+    using Last = std::integral_constant<bool, true>;
+    for (;;) {
+      if (it + 1 >= ntile) break;
+      step(NotLast{}, sa, sb);
+      if (it + 1 >= ntile) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) sa[mb] = sb[mb];
+        break;
+      }
+      step(NotLast{}, sb, sa);
     }
+    step(Last{}, sa, sb);
 
     // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
     // r4 of block db holds d = 32 db + 8 r4 + 4 hl + (0..3); lanes l and
@@ -935,7 +1056,7 @@ void tree_attn_kernel(const KParams args) {
     // d: lane hl = 0 the even groups, hl = 1 the odd ones.
     const float l = lsum + __shfl_xor(lsum, 32);
     const float linv = l > 0.f ? 1.0f / l : 0.f;
-    TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(sg.start + ql) * p.o_st + (int64_t)head * p.o_sh;
+    TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(cur.start + ql) * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -947,6 +1068,8 @@ void tree_attn_kernel(const KParams args) {
         for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) got.w[w4] = __shfl_xor(give.w[w4], 32);
         if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), hl ? got : keep, hl ? keep : got);
       }
+    gbase += ntile;
+    pre = nn;
   }  // units
 }
 
