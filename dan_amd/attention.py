@@ -25,6 +25,7 @@ unsupported shape raise.
 import functools
 import math
 from dataclasses import dataclass, field
+from typing import List
 
 import torch
 
@@ -276,15 +277,6 @@ def _past_table(plan, layer, hkv, d, dtype, device):
     return plan.past_tables[layer]
 
 
-def _workspace(plan, nbytes, device):
-    """Device scratch for the kernel's fp16 V^T copy, cached on the plan and
-    reused by every layer (launches are ordered on the stream)."""
-    ws = plan.workspace.get(nbytes)
-    if ws is None:
-        ws = plan.workspace[nbytes] = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    return ws
-
-
 @functools.lru_cache(maxsize=None)
 def _num_cus(device):
     """Compute units of the device (the persistent grid's size)."""
@@ -297,6 +289,12 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     attention launch alone with PHASE_ATTEND after a full call. ``noalloc``
     launches through ``dan_tree_attn_fwd_noalloc`` (the V^T copy in the
     library's own per-GPU scratch instead of a workspace)."""
+    return torch.ops.dan_amd.tree_attn(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc))
+
+
+def _op_args(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL, noalloc=False):
+    """Checks the inputs, builds (or finds) the batch's plan and the layer's
+    prefix-cache table, and returns the arguments of ``tree_attn``."""
     if not q.is_cuda:
         raise RuntimeError("dan_amd.attend runs on a gfx950 GPU only; got tensors on "
                            f"{q.device} (the masked CPU path is the test oracle, not a backend)")
@@ -314,40 +312,81 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     groups = _native.head_groups(h, hkv, lib)
     plan = get_plan(segments, n, tile_q, q.device, groups=groups, num_cus=_num_cus(q.device))
     table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
-    out_dtype = torch.bfloat16 if q.dtype == E4M3 else q.dtype
     if q.dtype == E4M3:
         q_scale, k_scale, v_scale = (_check_scale(t, nm, q.device) for t, nm in zip(fp8_scales, ("q_scale", "k_scale", "v_scale")))
     qk_dtype = _qk_dtype(q.dtype)
     q, k, v = _kernel_view(q.to(qk_dtype)), _kernel_view(k.to(qk_dtype)), _kernel_view(v)
-    out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
+    units, sched_off, slots = plan.schedule(groups, _num_cus(q.device)) if plan.num_work else (None, None, 0)
+    tables = [plan.segs_d, plan.work_d, plan.key_lo_d, plan.col_seg_d, table]
     if plan.num_work:
-        nbytes = _native.workspace_size(hkv, d, plan.vt_cols, lib)
-        ws = None if noalloc else _workspace(plan, nbytes, q.device)
+        tables += [units, sched_off]
+    scales = [q_scale, k_scale, v_scale] if q.dtype == E4M3 else []
+    meta = [len(plan.segs), len(plan.past_dicts), plan.num_work, tile_q, plan.vt_cols, slots, phases, int(noalloc)]
+    softmax_scale = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+    return q, k, v, tables, scales, meta, softmax_scale
+
+
+def _out_dtype(q, v):
+    """The kernel's output type: bf16 for e4m3 inputs, fp32 for fp32 v, else q's."""
+    return torch.bfloat16 if q.dtype == E4M3 else v.dtype if v.dtype == torch.float32 else q.dtype
+
+
+@torch.library.custom_op("dan_amd::tree_attn", mutates_args=(), device_types="cuda")
+def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[torch.Tensor],
+              scales: List[torch.Tensor], meta: List[int], scale: float) -> torch.Tensor:
+    """The kernel launch as a torch operator (``torch.ops.dan_amd.tree_attn``),
+    so that fake-tensor tracing and ``torch.compile`` see its output's shape,
+    dtype and strides without running it.
+
+    q [H, N, D], k and v [Hkv, N, D] in the kernel's types (q and k bf16,
+    fp16 or e4m3; v the same, or fp32 with fp16 q and k), rows 16-byte
+    aligned; ``tables``: the plan's device tables (segments, work items,
+    key_lo, col_seg), the layer's prefix-cache table and, when there is work,
+    the schedule (unit records, slot offsets); ``scales``: q, k, v scales of
+    e4m3 inputs; ``meta``: [segments, prefix entries, work items, tile_q,
+    V^T columns, slots, phases, noalloc]. Returns [H, N, D], a view of
+    token-major [N, H, D] storage. The V^T workspace comes from torch's
+    caching allocator on the current stream (stream-ordered reuse); with
+    ``noalloc`` the library's own scratch is used instead."""
+    lib = _native.load()
+    h, n, d = q.shape
+    hkv = k.shape[0]
+    num_segments, num_pasts, num_work, tile_q, vt_cols, slots, phases, noalloc = meta
+    out = torch.empty((n, h, d), dtype=_out_dtype(q, v), device=q.device)
+    if num_work:
+        segs_d, work_d, key_lo_d, col_seg_d, past_table, units, sched_off = tables
+        nbytes = _native.workspace_size(hkv, d, vt_cols, lib)
+        ws = None if noalloc else torch.empty(nbytes, dtype=torch.uint8, device=q.device)
         a = _native.DanTreeAttnArgs()
         a.abi_version = _native.ABI_VERSION
-        a.in_dtype = _DTYPES[qk_dtype]
+        a.in_dtype = _DTYPES[q.dtype]
         a.v_dtype = _DTYPES[v.dtype]
-        a.out_dtype = _DTYPES[out_dtype]
+        a.out_dtype = _DTYPES[out.dtype]
         a.num_heads, a.num_kv_heads, a.head_dim, a.num_tokens = h, hkv, d, n
-        a.scale = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+        a.scale = scale
         a.q, a.q_stride_tok, a.q_stride_head = q.data_ptr(), q.stride(1), q.stride(0)
         a.k, a.k_stride_tok, a.k_stride_head = k.data_ptr(), k.stride(1), k.stride(0)
         a.v, a.v_stride_tok, a.v_stride_head = v.data_ptr(), v.stride(1), v.stride(0)
         a.out, a.o_stride_tok, a.o_stride_head = out.data_ptr(), out.stride(0), out.stride(1)
-        a.segments, a.num_segments = plan.segs_d.data_ptr(), len(plan.segs)
-        a.pasts, a.num_pasts = table.data_ptr(), len(plan.past_dicts)
-        a.work, a.num_work = plan.work_d.data_ptr(), plan.num_work
-        a.key_lo = plan.key_lo_d.data_ptr()
+        a.segments, a.num_segments = segs_d.data_ptr(), num_segments
+        a.pasts, a.num_pasts = past_table.data_ptr(), num_pasts
+        a.work, a.num_work = work_d.data_ptr(), num_work
+        a.key_lo = key_lo_d.data_ptr()
         a.tile_q = tile_q
-        a.vt_cols = plan.vt_cols
-        a.col_seg = plan.col_seg_d.data_ptr()
+        a.vt_cols = vt_cols
+        a.col_seg = col_seg_d.data_ptr()
         if ws is not None:
             a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
         if q.dtype == E4M3:
-            a.q_scale, a.k_scale, a.v_scale = q_scale.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr()
+            a.q_scale, a.k_scale, a.v_scale = (t.data_ptr() for t in scales)
         a.phases = phases
-        units, sched_off, slots = plan.schedule(groups, _num_cus(q.device))
         a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
         launch = _native.forward_noalloc if noalloc else _native.forward
         launch(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)
+
+
+@tree_attn.register_fake
+def _tree_attn_fake(q, k, v, tables, scales, meta, scale):
+    h, n, d = q.shape
+    return q.new_empty((n, h, d), dtype=_out_dtype(q, v)).transpose(0, 1)

@@ -247,7 +247,6 @@ class TilePlan:
     key_lo_d: object = None
     col_seg_d: object = None
     past_tables: dict = field(default_factory=dict)  # layer -> (device bytes, keep-alive refs)
-    workspace: dict = field(default_factory=dict)  # bytes -> device scratch (reused by every layer)
     schedules: dict = field(default_factory=dict)  # (groups, CUs) -> (units_d, sched_off_d, slots)
 
     @classmethod

@@ -38,3 +38,25 @@ def test_cpu_tensors_raise():
 def test_batch_caches():
     b = A.Batch()
     assert b.layout is None and b.recurrent is None and b.tile_plan is None
+
+
+@pytest.mark.parametrize("qdt,vdt,want", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                          (torch.float16, torch.float16, torch.float16),
+                                          (torch.float16, torch.float32, torch.float32),
+                                          (torch.float8_e4m3fn, torch.float8_e4m3fn, torch.bfloat16)])
+def test_custom_op_fake_output(qdt, vdt, want):
+    """torch.ops.dan_amd.tree_attn under fake tensors (no GPU, no launch):
+    the output is [H, N, D] in the kernel's output type, a view of
+    token-major [N, H, D] storage -- the layout the real op returns."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    h, hkv, n, d = 32, 8, 100, 128
+    with FakeTensorMode():
+        q = torch.empty(h, n, d, dtype=qdt, device="cuda")
+        k = torch.empty(hkv, n, d, dtype=qdt, device="cuda")
+        v = torch.empty(hkv, n, d, dtype=vdt, device="cuda")
+        tables = [torch.empty(8, dtype=torch.int32, device="cuda") for _ in range(7)]
+        scales = [torch.empty(1, device="cuda") for _ in range(3)] if qdt == torch.float8_e4m3fn else []
+        o = torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, [1, 0, 1, 64, 128, 1, 0, 0], 0.1)
+        assert o.shape == (h, n, d) and o.dtype == want and o.device.type == "cuda"
+        assert o.stride() == (d, h * d, 1)
