@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 KEY_TILE = 64
 SCRATCH_BYTES = 32 << 20  # DAN_TREE_ATTN_SCRATCH_BYTES: dan_tree_attn_fwd_noalloc's V^T scratch per GPU
 
@@ -73,6 +73,14 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("col_seg", _vp),
                 ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32),
                 ("units", _vp), ("sched_off", _vp), ("num_slots", _i32)]
+
+
+STAGE_PARTIALS = 1024  # DAN_TREE_ATTN_STAGE_PARTIALS
+
+
+class DanStageF16Args(ctypes.Structure):
+    _fields_ = [("abi_version", _i32), ("d0", _i32), ("d1", _i32), ("d2", _i32), ("x", _vp),
+                ("stride0", _i64), ("stride1", _i64), ("out", _vp), ("scale", _vp), ("partial", _vp)]
 
 
 FRONT_ABI_VERSION = 1
@@ -140,7 +148,7 @@ class DanGdnConvArgs(ctypes.Structure):
                 ("beta", _vp), ("g", _vp)]
 
 
-EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_fwd_noalloc", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
+EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_fwd_noalloc", "dan_tree_attn_stage_f16", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
            "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
            "dan_fp8_quantize", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version",
@@ -166,6 +174,8 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_fwd.restype = ctypes.c_int
         lib.dan_tree_attn_fwd_noalloc.argtypes = [ctypes.POINTER(DanTreeAttnArgs), _vp]
         lib.dan_tree_attn_fwd_noalloc.restype = ctypes.c_int
+        lib.dan_tree_attn_stage_f16.argtypes = [ctypes.POINTER(DanStageF16Args), _vp]
+        lib.dan_tree_attn_stage_f16.restype = ctypes.c_int
         lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
         lib.dan_tree_attn_tile_q.restype = ctypes.c_int
         lib.dan_tree_attn_head_groups.argtypes = [_i32, _i32]
@@ -227,6 +237,14 @@ def head_groups(num_heads, num_kv_heads, lib=None):
 def workspace_size(num_kv_heads, head_dim, vt_cols, lib=None):
     """Bytes of device workspace one launch needs (0: invalid arguments)."""
     return (lib or load()).dan_tree_attn_workspace_size(num_kv_heads, head_dim, vt_cols)
+
+
+def stage_f16(args, stream, lib=None):
+    """Launch the fp32 -> fp16 staging; raises RuntimeError on failure."""
+    lib = lib or load()
+    rc = lib.dan_tree_attn_stage_f16(ctypes.byref(args), _vp(stream))
+    if rc != OK:
+        raise RuntimeError(f"dan_tree_attn_stage_f16 failed (status {rc}): {last_error(lib)}")
 
 
 def forward(args, stream, lib=None):

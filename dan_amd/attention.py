@@ -25,7 +25,7 @@ unsupported shape raise.
 import functools
 import math
 from dataclasses import dataclass, field
-from typing import List
+from typing import List, Optional
 
 import torch
 
@@ -232,8 +232,25 @@ def get_plan(segments, num_tokens, tile_q, device, groups=None, num_cus=None, pl
 
 
 def _qk_dtype(dtype):
-    """Matrix-core type of q and k: fp32 models stage them as fp16 (|x| < 65504)."""
+    """Matrix-core type of q and k: fp32 callers' are staged as fp16 (``_stage_f16``)."""
     return torch.float16 if dtype == torch.float32 else dtype
+
+
+def _stage_f16(x):
+    """fp32 [d0, d1, d2] -> (fp16 copy, scale) with x = copy * scale, scale a
+    power of 2 that keeps the copy within fp16's range
+    (``dan_tree_attn_stage_f16``, two launches on the current stream)."""
+    x = _kernel_view(x)
+    out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    scale = torch.empty(1, dtype=torch.float32, device=x.device)
+    partial = torch.empty(_native.STAGE_PARTIALS, dtype=torch.float32, device=x.device)
+    a = _native.DanStageF16Args()
+    a.abi_version = _native.ABI_VERSION
+    a.d0, a.d1, a.d2 = x.shape
+    a.x, a.stride0, a.stride1 = x.data_ptr(), x.stride(0), x.stride(1)
+    a.out, a.scale, a.partial = out.data_ptr(), scale.data_ptr(), partial.data_ptr()
+    _native.stage_f16(a, torch.cuda.current_stream(x.device).cuda_stream)
+    return out, scale
 
 
 def _past_table(plan, layer, hkv, d, dtype, device):
@@ -262,7 +279,11 @@ def _past_table(plan, layer, hkv, d, dtype, device):
             raise ValueError(f"past entry {i}, layer {layer}: k {tuple(pk.shape)}, v {tuple(pv.shape)}; want [Hkv, P, D]")
         if pk.dtype != dtype or pv.dtype != dtype or pk.device != device or pv.device != device:
             raise ValueError(f"past entry {i}, layer {layer}: dtype/device must match q")
-        pk, pv = _kernel_view(pk.to(_qk_dtype(dtype))), _kernel_view(pv)
+        if dtype == torch.float32:
+            pk, pks = _stage_f16(pk)
+            refs.append(pks)
+            descs[i].k_scale = pks.data_ptr()
+        pk, pv = _kernel_view(pk), _kernel_view(pv)
         refs += [pk, pv]
         descs[i].k, descs[i].v = pk.data_ptr(), pv.data_ptr()
         descs[i].k_stride_head, descs[i].k_stride_tok = pk.stride(0), pk.stride(1)
@@ -283,13 +304,31 @@ def _num_cus(device):
     return torch.cuda.get_device_properties(device).multi_processor_count
 
 
-def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL, noalloc=False):
+def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL, noalloc=False,
+                  workspace=None):
     """The kernel call behind ``attend`` (no save side effect). ``phases``
-    selects the launches (the C ABI's ``phases``): bench.py times the
-    attention launch alone with PHASE_ATTEND after a full call. ``noalloc``
-    launches through ``dan_tree_attn_fwd_noalloc`` (the V^T copy in the
-    library's own per-GPU scratch instead of a workspace)."""
-    return torch.ops.dan_amd.tree_attn(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc))
+    selects the launches (the C ABI's ``phases``); a split call passes its own
+    ``workspace`` (``workspace_bytes`` bytes of uint8 on the device) so that
+    the attention-only launch reads the V^T copy an earlier PHASE_PACK or full
+    call wrote there -- bench.py times the attention launch alone that way.
+    ``noalloc`` launches through ``dan_tree_attn_fwd_noalloc`` (the V^T copy in
+    the library's own per-GPU scratch instead of a workspace)."""
+    if phases != _native.PHASES_ALL and workspace is None and not noalloc:
+        raise ValueError("a split call (PHASE_PACK / PHASE_ATTEND) needs the workspace the two phases share")
+    return torch.ops.dan_amd.tree_attn(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc),
+                                       workspace)
+
+
+def workspace_bytes(q, k, segments):
+    """Bytes of the V^T workspace of a split ``_attend_fused`` call on this
+    batch (the plan is built or found as for the call itself)."""
+    h, n, d = q.shape
+    hkv = k.shape[0]
+    lib = _native.load()
+    tile_q = _native.tile_q(h, hkv, lib)
+    groups = _native.head_groups(h, hkv, lib)
+    plan = get_plan(segments, n, tile_q, q.device, groups=groups, num_cus=_num_cus(q.device))
+    return _native.workspace_size(hkv, d, plan.vt_cols, lib)
 
 
 def _op_args(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PHASES_ALL, noalloc=False):
@@ -314,13 +353,15 @@ def _op_args(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PH
     table, _refs = _past_table(plan, layer, hkv, d, q.dtype, q.device)
     if q.dtype == E4M3:
         q_scale, k_scale, v_scale = (_check_scale(t, nm, q.device) for t, nm in zip(fp8_scales, ("q_scale", "k_scale", "v_scale")))
-    qk_dtype = _qk_dtype(q.dtype)
-    q, k, v = _kernel_view(q.to(qk_dtype)), _kernel_view(k.to(qk_dtype)), _kernel_view(v)
+    scales = [q_scale, k_scale, v_scale] if q.dtype == E4M3 else []
+    if q.dtype == torch.float32:  # fp16 for the matrix core, with power-of-2 scales
+        (q, q_scale), (k, k_scale) = _stage_f16(q), _stage_f16(k)
+        scales = [q_scale, k_scale]
+    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
     units, sched_off, slots = plan.schedule(groups, _num_cus(q.device)) if plan.num_work else (None, None, 0)
     tables = [plan.segs_d, plan.work_d, plan.key_lo_d, plan.col_seg_d, table]
     if plan.num_work:
         tables += [units, sched_off]
-    scales = [q_scale, k_scale, v_scale] if q.dtype == E4M3 else []
     meta = [len(plan.segs), len(plan.past_dicts), plan.num_work, tile_q, plan.vt_cols, slots, phases, int(noalloc)]
     softmax_scale = (1.0 / math.sqrt(d)) if scale is None else float(scale)
     return q, k, v, tables, scales, meta, softmax_scale
@@ -331,9 +372,10 @@ def _out_dtype(q, v):
     return torch.bfloat16 if q.dtype == E4M3 else v.dtype if v.dtype == torch.float32 else q.dtype
 
 
-@torch.library.custom_op("dan_amd::tree_attn", mutates_args=(), device_types="cuda")
+@torch.library.custom_op("dan_amd::tree_attn", mutates_args=("workspace",), device_types="cuda")
 def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[torch.Tensor],
-              scales: List[torch.Tensor], meta: List[int], scale: float) -> torch.Tensor:
+              scales: List[torch.Tensor], meta: List[int], scale: float,
+              workspace: Optional[torch.Tensor]) -> torch.Tensor:
     """The kernel launch as a torch operator (``torch.ops.dan_amd.tree_attn``),
     so that fake-tensor tracing and ``torch.compile`` see its output's shape,
     dtype and strides without running it.
@@ -343,11 +385,13 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
     aligned; ``tables``: the plan's device tables (segments, work items,
     key_lo, col_seg), the layer's prefix-cache table and, when there is work,
     the schedule (unit records, slot offsets); ``scales``: q, k, v scales of
-    e4m3 inputs; ``meta``: [segments, prefix entries, work items, tile_q,
+    e4m3 inputs, or the power-of-2 q and k scales of fp32 inputs staged to fp16; ``meta``: [segments, prefix entries, work items, tile_q,
     V^T columns, slots, phases, noalloc]. Returns [H, N, D], a view of
-    token-major [N, H, D] storage. The V^T workspace comes from torch's
-    caching allocator on the current stream (stream-ordered reuse); with
-    ``noalloc`` the library's own scratch is used instead."""
+    token-major [N, H, D] storage. The V^T copy goes to ``workspace`` when the
+    caller passes one (uint8, at least ``dan_tree_attn_workspace_size`` bytes;
+    written by the copy, read by the attention launch), else to a block of
+    torch's caching allocator on the current stream (stream-ordered reuse);
+    with ``noalloc`` the library's own scratch is used instead."""
     lib = _native.load()
     h, n, d = q.shape
     hkv = k.shape[0]
@@ -356,7 +400,11 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
     if num_work:
         segs_d, work_d, key_lo_d, col_seg_d, past_table, units, sched_off = tables
         nbytes = _native.workspace_size(hkv, d, vt_cols, lib)
-        ws = None if noalloc else torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        ws = None
+        if not noalloc:
+            ws = workspace if workspace is not None else torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+            if ws.dtype != torch.uint8 or ws.device != q.device or not ws.is_contiguous() or ws.numel() < nbytes:
+                raise ValueError(f"workspace: a contiguous uint8 tensor of >= {nbytes} bytes on {q.device}")
         a = _native.DanTreeAttnArgs()
         a.abi_version = _native.ABI_VERSION
         a.in_dtype = _DTYPES[q.dtype]
@@ -377,8 +425,10 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
         a.col_seg = col_seg_d.data_ptr()
         if ws is not None:
             a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
-        if q.dtype == E4M3:
-            a.q_scale, a.k_scale, a.v_scale = (t.data_ptr() for t in scales)
+        if scales:  # e4m3: q, k, v; fp32 staged to fp16: q, k
+            a.q_scale, a.k_scale = scales[0].data_ptr(), scales[1].data_ptr()
+            if len(scales) == 3:
+                a.v_scale = scales[2].data_ptr()
         a.phases = phases
         a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
         launch = _native.forward_noalloc if noalloc else _native.forward
@@ -387,6 +437,6 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
 
 
 @tree_attn.register_fake
-def _tree_attn_fake(q, k, v, tables, scales, meta, scale):
+def _tree_attn_fake(q, k, v, tables, scales, meta, scale, workspace):
     h, n, d = q.shape
     return q.new_empty((n, h, d), dtype=_out_dtype(q, v)).transpose(0, 1)

@@ -54,6 +54,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "dan_tree_attn.h"
@@ -115,6 +116,7 @@ struct KParams {
   const void *q, *k;
   void *o;
   const _Float16 *vt;
+  const int32_t *vexp;  // per V^T column block: the copy holds V * 2^-vexp
   int64_t q_st, q_sh, k_st, k_sh, o_st, o_sh;
   const DanPastDesc *pasts;
   const int32_t *key_lo;
@@ -139,6 +141,7 @@ struct PackParams {
   const DanPastDesc *pasts;
   const int32_t *col_seg;
   _Float16 *vt;
+  int32_t *vexp;  // [Hkv][vt_cols / 64]: power-of-2 exponent of each column block (V^T = V * 2^-e)
   int32_t num_kv_heads, vt_cols;
   const float *v_scale;  // e4m3 only: per-tensor scale of v (prefix-cache entries carry their own)
 };
@@ -200,38 +203,6 @@ __device__ inline T load_scalar(const T *p) {
 #pragma unroll
   for (int i = 0; i < (int)(sizeof(T) / 4); ++i) raw.w[i] = __builtin_amdgcn_readfirstlane(src[i]);
   return __builtin_bit_cast(T, raw);
-}
-
-// 8 consecutive input elements -> 8 compute-type elements (16 bytes).
-template <typename TIn, typename TC>
-__device__ inline u32x4 load8(const TIn *p);
-
-template <>
-__device__ inline u32x4 load8<__bf16, __bf16>(const __bf16 *p) {
-  return *gbl(reinterpret_cast<const u32x4 *>(p));
-}
-template <>
-__device__ inline u32x4 load8<_Float16, _Float16>(const _Float16 *p) {
-  return *gbl(reinterpret_cast<const u32x4 *>(p));
-}
-template <>
-__device__ inline u32x4 load8<float, _Float16>(const float *p) {
-  const f32x4 a = *gbl(reinterpret_cast<const f32x4 *>(p));
-  const f32x4 b = *gbl(reinterpret_cast<const f32x4 *>(p + 4));
-  const f32x8 x = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  return __builtin_bit_cast(u32x4, __builtin_convertvector(x, f16x8));
-}
-// bf16 -> fp16 is exact for magnitudes in fp16's normal range [2^-14, 65504].
-template <>
-__device__ inline u32x4 load8<__bf16, _Float16>(const __bf16 *p) {
-  const u32x4 v = *gbl(reinterpret_cast<const u32x4 *>(p));
-  f32x8 x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
-    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
-  }
-  return __builtin_bit_cast(u32x4, __builtin_convertvector(x, f16x8));
 }
 
 // 8 e4m3 values (8 bytes) -> 8 fp32 values.
@@ -511,16 +482,53 @@ __host__ __device__ constexpr int kswz(int m) {
 // from v; zero past the segment's end), converts them to fp16 and writes them
 // transposed, as the P V operand fragments of the block (16 KB contiguous per
 // block and kv head at D = 128; see Lds).
-// 8 consecutive values of v times `scale` (e4m3 only) -> 8 fp16 values.
+// 8 consecutive values of v (times `scale`, e4m3 only) as fp32.
 template <typename TV>
-__device__ inline u32x4 load8_v(const TV *p, float) {
-  return load8<TV, _Float16>(p);
+__device__ inline f32x8 load8_f32(const TV *p, float scale);
+template <>
+__device__ inline f32x8 load8_f32<__bf16>(const __bf16 *p, float) {
+  const u32x4 v = *gbl(reinterpret_cast<const u32x4 *>(p));
+  f32x8 x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __builtin_bit_cast(float, v[i] << 16);
+    x[2 * i + 1] = __builtin_bit_cast(float, v[i] & 0xffff0000u);
+  }
+  return x;
 }
 template <>
-__device__ inline u32x4 load8_v<E4M3>(const E4M3 *p, float scale) {
-  const f32x8 x = e4m3x8_to_f32(*gbl(reinterpret_cast<const u32x2 *>(p))) * scale;
-  return __builtin_bit_cast(u32x4, __builtin_convertvector(x, f16x8));
+__device__ inline f32x8 load8_f32<_Float16>(const _Float16 *p, float) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x8, *gbl(reinterpret_cast<const u32x4 *>(p))), f32x8);
 }
+template <>
+__device__ inline f32x8 load8_f32<float>(const float *p, float) {
+  const f32x4 a = *gbl(reinterpret_cast<const f32x4 *>(p));
+  const f32x4 b = *gbl(reinterpret_cast<const f32x4 *>(p + 4));
+  return f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+template <>
+__device__ inline f32x8 load8_f32<E4M3>(const E4M3 *p, float scale) {
+  return e4m3x8_to_f32(*gbl(reinterpret_cast<const u32x2 *>(p))) * scale;
+}
+
+// Power-of-2 exponent e of a V^T column block from its largest magnitude:
+// the copy holds V * 2^-e in fp16. e = 0 while the largest |v| lies in
+// [2^-6, 2^15] (bf16 and fp16 inputs there convert exactly, or lose only
+// fp16 subnormal bits far below the block's largest value); otherwise e
+// brings it into (2^14, 2^15], so fp16 neither overflows nor flushes the
+// block. A zero, inf or NaN maximum keeps e = 0 (NaN and inf propagate).
+// e is clamped to [-60, 60]: blocks with |v| up to 2^75 stay finite.
+__host__ __device__ inline int vt_exponent(float amax) {
+  uint32_t b;
+  memcpy(&b, &amax, 4);
+  const int bexp = (int)((b >> 23) & 0xff);
+  if (bexp == 0xff || b == 0 || (amax >= 0x1p-6f && amax <= 0x1p15f)) return 0;
+  const int ceil_log2 = bexp == 0 ? -126 : (bexp - 127) + ((b & 0x7fffff) != 0);
+  const int e = ceil_log2 - 15;
+  return e < -60 ? -60 : e > 60 ? 60 : e;  // any two differ by at most 120: 2^(e1 - e2) stays a normal fp32
+}
+// 2^e as an fp32 (exact for e in [-126, 127]).
+__device__ inline float exp2i(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
 
 template <typename TV, int D>
 __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
@@ -531,6 +539,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   // a row together and makes both phases conflict-free: each half-wave writes
   // 8 d chunks x 4 key pairs to 32 distinct banks, and 8 lanes read one row.
   __shared__ __attribute__((aligned(16))) uint32_t tile[D * 32];
+  __shared__ float wave_max[4];
   const int kvh = blockIdx.x % p.num_kv_heads, cb = blockIdx.x / p.num_kv_heads;
   const DanSegmentDesc sg = load_entry(p.segs + *gbl(p.col_seg + cb));
   const int key0 = cb * kKeyTile - sg.vt_col;
@@ -546,7 +555,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     pv_st = pd.v_stride_tok;
     if (kF8) pvs = *gbl(pd.v_scale);
   }
-  // 8 values of key `key` (segment key coordinates) from d chunk c, as fp16.
+  // 8 values of key `key` (segment key coordinates) from d chunk c, as fp32.
   // Branch-free: a key past the segment reads a stand-in row (the segment's
   // first past or new row, which exists since the column block does) and is
   // zeroed, so every thread's loads are in flight together (a load under a
@@ -555,12 +564,12 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   auto row8 = [&](int key, int c) __attribute__((always_inline)) {
     const bool past = key < P, valid = key < PN;
     const TV *src = !valid ? first : past ? pvp + (int64_t)key * pv_st : vp + (int64_t)(sg.start + key - P) * p.v_st;
-    const u32x4 x = load8_v<TV>(src + 8 * c, past ? pvs : vs);
-    return valid ? x : u32x4{0, 0, 0, 0};
+    const f32x8 x = load8_f32<TV>(src + 8 * c, past ? pvs : vs);
+    return valid ? x : f32x8{};
   };
   const int hw = threadIdx.x >> 5, j = threadIdx.x & 31;  // half-wave, lane in it
   const int c_lo = j >> 2, kp_lo = j & 3;
-  u32x4 r0[kPasses], r1[kPasses];
+  f32x8 r0[kPasses], r1[kPasses];
 #pragma unroll
   for (int pass = 0; pass < kPasses; ++pass) {  // all loads in flight first
     const int item = hw + 8 * pass;
@@ -569,11 +578,24 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
     r1[pass] = row8(key0 + 2 * kp + 1, c);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // The block's largest magnitude (NaN-ignoring max) -> its exponent.
+  float m = 0.f;
+#pragma unroll
+  for (int pass = 0; pass < kPasses; ++pass)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fmaxf(fabsf(r0[pass][e]), fabsf(r1[pass][e])));
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = m;
+  __syncthreads();
+  const int ex = vt_exponent(fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3])));
+  const float down = exp2i(-ex);
+  if (threadIdx.x == 0) p.vexp[(int64_t)kvh * (p.vt_cols / kKeyTile) + cb] = ex;
 #pragma unroll
   for (int pass = 0; pass < kPasses; ++pass) {
     const int item = hw + 8 * pass;
     const int c = c_lo + 8 * (item / 8), kp = kp_lo + 4 * (item % 8);
-    const f16x8 a = __builtin_bit_cast(f16x8, r0[pass]), b = __builtin_bit_cast(f16x8, r1[pass]);
+    const f16x8 a = __builtin_convertvector(r0[pass] * down, f16x8), b = __builtin_convertvector(r1[pass] * down, f16x8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const f16x2 pr = {a[e], b[e]};
@@ -785,6 +807,8 @@ void tree_attn_kernel(const KParams args) {
     const int kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
     const Src cur = make_src(p, un);
     const int P = cur.P, PT = P + un.trunk, ntile = cur.ntile;
+    // exponents of this unit's V^T column blocks (tile j: vexp_u[j])
+    const int32_t *vexp_u = p.vexp + ((int64_t)kvh * (p.vt_cols / kKeyTile) + un.vt_col / kKeyTile);
     uint32_t off_b[SLOTS];
     past_offsets(cur.pk_st, off_b);
     // The next unit, whose first tiles (nn of them) this unit's last steps
@@ -815,9 +839,10 @@ void tree_attn_kernel(const KParams args) {
     const bool wave_work = hig < p.rep && qw0 < qend;
 
     // Softmax exponent factor c of S: scale * log2(e), times q_scale * k_scale
-    // for e4m3 (the prefix-cache entry's k has its own scale, c_past).
+    // for scaled inputs -- e4m3, and fp32 q / k staged to fp16 with power-of-2
+    // scales (the prefix-cache entry's k has its own scale, c_past).
     float c_new = p.c, c_past = p.c;
-    if (kF8) {
+    if (kF8 || p.q_scale) {
       const float qs = load_scalar(p.q_scale);
       c_new = c_past = p.c * qs * load_scalar(p.k_scale);
       if (P > 0) c_past = p.c * qs * load_scalar(load_scalar(p.pasts + un.past_idx).k_scale);
@@ -834,6 +859,9 @@ void tree_attn_kernel(const KParams args) {
 #pragma unroll
     for (int db = 0; db < ND; ++db) o[db] = f32x16{};
     float mneg, lsum = 0.f;  // exponent offset -m of the running max m
+    // O holds O_true * 2^-vE: the exponent of the V^T blocks it was last
+    // accumulated from (0 unless a block of this unit needed one).
+    int vE = 0;
     u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
     // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
@@ -887,13 +915,13 @@ void tree_attn_kernel(const KParams args) {
           }
       }
     };
-    // Exponent factor of tile j's scores, and (e4m3) the fix-up of a tile that
-    // holds both prefix-cache and new keys: the prefix keys' scores are brought
-    // to the new keys' k scale, and the tile then uses c_new.
+    // Exponent factor of tile j's scores, and (scaled inputs) the fix-up of a
+    // tile that holds both prefix-cache and new keys: the prefix keys' scores
+    // are brought to the new keys' k scale, and the tile then uses c_new.
     auto tile_c = [&](int j) __attribute__((always_inline)) { return j * kKeyTile + kKeyTile <= P ? c_past : c_new; };
     auto fix_straddle = [&](int j, f32x16(&s)[2]) __attribute__((always_inline)) {
       const int kb = j * kKeyTile;
-      if (!kF8 || !(kb < P && kb + kKeyTile > P)) return;
+      if (c_past == c_new || !(kb < P && kb + kKeyTile > P)) return;
       const float ratio = c_past / c_new;
       const int lim = P - kb - 8 * hl;  // prefix key: rel < lim
 #pragma unroll
@@ -947,21 +975,30 @@ void tree_attn_kernel(const KParams args) {
       return (acc[0] + acc[1]) + (acc[2] + acc[3]);
     };
     // Accept the tile's P (partial sum ts), raising m to the tile's max (and
-    // redoing P) first if it overflowed.
-    auto finish_tile = [&](const f32x16(&s)[2], float ts, float c) __attribute__((always_inline)) {
-      if (__any(!(ts <= kSumLimit))) {
-        const float mold = -mneg;
-        const float mnew = fmaxf(mold, s_max(s) * c);
-        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
-        mneg = -mnew;
-        lsum *= alpha;
+    // redoing P) first if it overflowed; and bring O to the scale of the
+    // tile's V^T block (2^ve) if it differs from O's (2^vE). Both are rare
+    // and share one branch.
+    auto finish_tile = [&](const f32x16(&s)[2], float ts, float c, int ve) __attribute__((always_inline)) {
+      const bool raise = __any(!(ts <= kSumLimit));
+      if (raise || ve != vE) {
+        float f = exp2i(vE - ve);
+        if (raise) {
+          const float mold = -mneg;
+          const float mnew = fmaxf(mold, s_max(s) * c);
+          const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+          mneg = -mnew;
+          lsum *= alpha;
+          f *= alpha;
+          ts = exp_phase(s, c);
+        }
 #pragma unroll
-        for (int db = 0; db < ND; ++db) o[db] *= alpha;
-        ts = exp_phase(s, c);
+        for (int db = 0; db < ND; ++db) o[db] *= f;
+        vE = ve;
       }
       lsum += ts;
     };
-    // O^T += V^T P^T over the 64 keys of stage buffer b.
+    // O^T += V^T P^T over the 64 keys of stage buffer b (its V^T block is at
+    // O's scale: finish_tile).
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
       const uint8_t *vbuf = smem + b * L::buf + v_lane;
 #pragma unroll
@@ -1019,6 +1056,7 @@ void tree_attn_kernel(const KParams args) {
         else wait_vmem<0>();
       }
       barrier_lds();
+      const int ve = load_scalar(vexp_u + tile_of(it));  // the tile's V^T exponent (finish_tile)
       // The issuing waves load tile it+3 now (see kIssuers).
       if (wave < kIssuers) issue_cat(it + 3);
       if (kLast && nn > 0) {  // q and key_lo of the next unit (this unit's are no longer used)
@@ -1028,7 +1066,7 @@ void tree_attn_kernel(const KParams args) {
       const float c = tile_c(tile_of(it));
       const float ts = exp_phase(cur_s, c);
       if (!kLast) qk_phase((gbase + it + 1) & 3, nxt_s);
-      finish_tile(cur_s, ts, c);
+      finish_tile(cur_s, ts, c, ve);
       pv_phase((gbase + it) & 3);
       if (!kLast) {
         mask_phase(tile_of(it + 1), nxt_s);
@@ -1055,7 +1093,7 @@ void tree_attn_kernel(const KParams args) {
     // l ^ 32 (the same query) trade halves so that each stores 8 contiguous
     // d: lane hl = 0 the even groups, hl = 1 the odd ones.
     const float l = lsum + __shfl_xor(lsum, 32);
-    const float linv = l > 0.f ? 1.0f / l : 0.f;
+    const float linv = l > 0.f ? exp2i(vE) / l : 0.f;
     TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(cur.start + ql) * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
@@ -1071,6 +1109,59 @@ void tree_attn_kernel(const KParams args) {
     gbase += ntile;
     pre = nn;
   }  // units
+}
+
+// ---------------------------------------------------------------- fp32 -> fp16 staging
+// q and k of fp32 callers become fp16 for the matrix core with a per-tensor
+// power-of-2 scale (x = out * scale, exact), so magnitudes beyond fp16's
+// range neither overflow nor flush. Two launches over the same grid: the
+// partial maxima, then every work group reduces them, takes the exponent
+// (vt_exponent's rule) and converts its share.
+struct StageParams {
+  const float *x;
+  int64_t s0, s1;  // strides of dims 0 and 1 (dim 2 contiguous)
+  int32_t d0, d1, d2;
+  _Float16 *out;   // [d0][d1][d2] contiguous
+  float *scale;    // receives 2^e
+  float *partial;  // [gridDim.x] partial maxima
+};
+
+__device__ inline float block_max256(float m, float *red) {
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void stage_max_kernel(const StageParams p) {
+  __shared__ float red[4];
+  const int c4 = p.d2 / 4;
+  const int64_t n = (int64_t)p.d0 * p.d1 * c4;
+  float m = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / c4;
+    const f32x4 v = *gbl(reinterpret_cast<const f32x4 *>(p.x + (r / p.d1) * p.s0 + (r % p.d1) * p.s1 + 4 * (i % c4)));
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  m = block_max256(m, red);
+  if (threadIdx.x == 0) p.partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(256) void stage_convert_kernel(const StageParams p) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < (int)gridDim.x; i += 256) m = fmaxf(m, *gbl(p.partial + i));
+  const int ex = vt_exponent(block_max256(m, red));
+  const float down = exp2i(-ex);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *gbl_mut(p.scale) = exp2i(ex);
+  const int c4 = p.d2 / 4;
+  const int64_t n = (int64_t)p.d0 * p.d1 * c4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / c4;
+    const f32x4 v = *gbl(reinterpret_cast<const f32x4 *>(p.x + (r / p.d1) * p.s0 + (r % p.d1) * p.s1 + 4 * (i % c4)));
+    *gbl_mut(reinterpret_cast<u32x2 *>(p.out + 4 * i)) = __builtin_bit_cast(u32x2, __builtin_convertvector(v * down, f16x4));
+  }
 }
 
 // ---------------------------------------------------------------- host side
@@ -1096,6 +1187,12 @@ int fail(int status, const char *fmt, ...) {
   vsnprintf(g_err, sizeof g_err, fmt, ap);
   va_end(ap);
   return status;
+}
+
+// Bytes of the fp16 V^T copy at the start of the workspace; the column
+// blocks' int32 exponents follow it.
+int64_t vt_bytes(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols) {
+  return (int64_t)num_kv_heads * head_dim * vt_cols * 2;
 }
 
 // Heads of one kv group that one work group covers: the 4 waves of a SIMD
@@ -1174,7 +1271,7 @@ int dan_tree_attn_head_groups(int32_t num_heads, int32_t num_kv_heads) {
 
 int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols) {
   if (num_kv_heads <= 0 || head_dim <= 0 || vt_cols < 0 || vt_cols % dan::kKeyTile) return 0;
-  return (int64_t)num_kv_heads * head_dim * vt_cols * 2;
+  return dan::vt_bytes(num_kv_heads, head_dim, vt_cols) + ((int64_t)num_kv_heads * (vt_cols / dan::kKeyTile) * 4 + 255) / 256 * 256;
 }
 
 int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
@@ -1205,6 +1302,8 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   if (a->num_pasts > 0 && !a->pasts) return fail(DAN_ERR_INVALID_ARGUMENT, "num_pasts > 0 with NULL pasts");
   if (f8 && (!a->q_scale || !a->k_scale || !a->v_scale))
     return fail(DAN_ERR_INVALID_ARGUMENT, "e4m3 inputs need q_scale, k_scale and v_scale");
+  if (!f8 && (!a->q_scale != !a->k_scale || (a->q_scale && !f32)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "q_scale and k_scale go together, and only with e4m3 or fp32-staged inputs");
   if (!finite_positive(a->scale)) return fail(DAN_ERR_INVALID_ARGUMENT, "scale must be finite and > 0");
   if (a->phases < DAN_TREE_ATTN_PHASES_ALL || a->phases > DAN_TREE_ATTN_PHASE_ATTEND)
     return fail(DAN_ERR_INVALID_ARGUMENT, "phases %d: 0 (all), 1 (pack) or 2 (attend)", a->phases);
@@ -1242,11 +1341,12 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   pp.v = a->v; pp.v_st = a->v_stride_tok; pp.v_sh = a->v_stride_head;
   pp.segs = a->segments; pp.pasts = a->pasts; pp.col_seg = a->col_seg;
   pp.vt = static_cast<_Float16 *>(a->workspace);
+  pp.vexp = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(a->workspace) + vt_bytes(Hkv, D, a->vt_cols));
   pp.num_kv_heads = Hkv; pp.vt_cols = a->vt_cols;
   pp.v_scale = a->v_scale;
 
   KParams kp;
-  kp.q = a->q; kp.k = a->k; kp.o = a->out; kp.vt = pp.vt;
+  kp.q = a->q; kp.k = a->k; kp.o = a->out; kp.vt = pp.vt; kp.vexp = pp.vexp;
   kp.q_st = a->q_stride_tok; kp.q_sh = a->q_stride_head;
   kp.k_st = a->k_stride_tok; kp.k_sh = a->k_stride_head;
   kp.o_st = a->o_stride_tok; kp.o_sh = a->o_stride_head;
@@ -1274,6 +1374,30 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   else if (f8) err = d128 ? launch_attn<E4M3, __bf16, 128>(kp, grid, s) : launch_attn<E4M3, __bf16, 64>(kp, grid, s);
   else err = d128 ? launch_attn<_Float16, float, 128>(kp, grid, s) : launch_attn<_Float16, float, 64>(kp, grid, s);
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
+  return DAN_OK;
+}
+
+int dan_tree_attn_stage_f16(const DanStageF16Args *a, void *stream) {
+  using namespace dan;
+  g_err[0] = 0;
+  if (!a) return fail(DAN_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->abi_version != DAN_TREE_ATTN_ABI_VERSION)
+    return fail(DAN_ERR_VERSION, "abi_version %d, library speaks %d", a->abi_version, DAN_TREE_ATTN_ABI_VERSION);
+  if (a->d0 < 0 || a->d1 < 0 || a->d2 < 0 || a->d2 % 4)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "shape [%d, %d, %d]: the last dimension must be a multiple of 4", a->d0, a->d1, a->d2);
+  if (!a->x || !a->out || !a->scale || !a->partial) return fail(DAN_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (((uintptr_t)a->x & 15) || ((uintptr_t)a->out & 7) || ((a->stride0 | a->stride1) & 3) || a->stride0 < 0 || a->stride1 < 0)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned with strides that keep rows 16-byte aligned, out 8-byte aligned");
+  StageParams sp;
+  sp.x = a->x; sp.s0 = a->stride0; sp.s1 = a->stride1; sp.d0 = a->d0; sp.d1 = a->d1; sp.d2 = a->d2;
+  sp.out = static_cast<_Float16 *>(a->out); sp.scale = a->scale; sp.partial = a->partial;
+  const int64_t n4 = (int64_t)a->d0 * a->d1 * (a->d2 / 4);
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(DAN_TREE_ATTN_STAGE_PARTIALS, (n4 + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(stage_max_kernel, dim3(grid), dim3(256), 0, s, sp);
+  hipLaunchKernelGGL(stage_convert_kernel, dim3(grid), dim3(256), 0, s, sp);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "staging launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
 }
 

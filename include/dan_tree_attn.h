@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 5
+#define DAN_TREE_ATTN_ABI_VERSION 6
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -80,7 +80,9 @@ typedef struct {
 /* One prefix-cache entry for the current layer: k, v each [Hkv, len, D]
  * (dan/cache.py:15, dan/attention.py:202-204, :254-257). Several segments may
  * point at the same entry. k_scale / v_scale are device fp32 scalars for
- * DAN_DTYPE_E4M3 and ignored otherwise. */
+ * DAN_DTYPE_E4M3 (k ~ kq * k_scale); with fp16 q and k staged from fp32
+ * (DanTreeAttnArgs.q_scale set), k_scale is the staged k's power-of-2 scale
+ * and v_scale is ignored; otherwise both are ignored. */
 typedef struct {
   const void *k;
   const void *v;
@@ -144,7 +146,11 @@ typedef struct {
   const void *v; int64_t v_stride_tok, v_stride_head; /* [N, Hkv, D] view */
   void *out;     int64_t o_stride_tok, o_stride_head; /* [N, H, D] view   */
 
-  /* DAN_DTYPE_E4M3 only: device fp32 per-tensor scales of q, k and v. */
+  /* Device fp32 per-tensor scales (x ~ stored * scale). DAN_DTYPE_E4M3:
+   * q_scale, k_scale and v_scale, all required. fp16 q and k with fp32 v
+   * (fp32 callers): optionally q_scale and k_scale together, the power-of-2
+   * scales dan_tree_attn_stage_f16 wrote, and then every prefix entry's
+   * k_scale too; S is multiplied by q_scale * k_scale. NULL otherwise. */
   const float *q_scale;
   const float *k_scale;
   const float *v_scale;
@@ -162,8 +168,10 @@ typedef struct {
   const int32_t *col_seg;
   /* Device scratch of at least dan_tree_attn_workspace_size() bytes, 256-byte
    * aligned, owned by the caller: it receives V (and the pasts' v) as fp16,
-   * transposed to [Hkv][D][vt_cols], before the attention kernel runs on the
-   * same stream. */
+   * transposed to [Hkv][D][vt_cols], and after it one int32 exponent per
+   * (kv head, 64-column block), before the attention kernel runs on the same
+   * stream. A block holds V * 2^-e: e = 0 unless its largest |v| lies outside
+   * [2^-6, 2^15], so no finite v overflows or flushes in fp16. */
   void *workspace;
   int64_t workspace_bytes;
   /* Which of the two launches to make: DAN_TREE_ATTN_PHASES_ALL (0: the V^T
@@ -197,6 +205,27 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *args, void *stream);
 
 /* Bytes of workspace dan_tree_attn_fwd needs (0 for invalid arguments). */
 int64_t dan_tree_attn_workspace_size(int32_t num_kv_heads, int32_t head_dim, int32_t vt_cols);
+
+/* fp32 -> fp16 staging of q or k for fp32 callers: out = x * 2^-e in fp16,
+ * *scale = 2^e, with e = 0 while max |x| lies in [2^-6, 2^15] and otherwise
+ * chosen to bring it into (2^14, 2^15] (so values beyond fp16's range neither
+ * overflow nor flush). Two launches on `stream`; `partial` is device scratch
+ * of DAN_TREE_ATTN_STAGE_PARTIALS floats. Replaces the reference's fp32
+ * inputs to attend (dan/attention.py:200) at full range: the matrix core has
+ * no fp32 product, and a plain cast to fp16 overflows beyond 65504.
+ * No reference counterpart as an entry point. */
+#define DAN_TREE_ATTN_STAGE_PARTIALS 1024
+typedef struct {
+  int32_t abi_version;          /* DAN_TREE_ATTN_ABI_VERSION */
+  int32_t d0, d1, d2;           /* shape; d2 a multiple of 4, contiguous */
+  const float *x;               /* 16-byte aligned */
+  int64_t stride0, stride1;     /* element strides of dims 0 and 1 (multiples of 4) */
+  void *out;                    /* fp16 [d0][d1][d2], contiguous */
+  float *scale;                 /* device fp32 scalar: receives 2^e */
+  float *partial;               /* device scratch, DAN_TREE_ATTN_STAGE_PARTIALS floats */
+} DanStageF16Args;
+
+int dan_tree_attn_stage_f16(const DanStageF16Args *args, void *stream);
 
 /* Capacity in bytes of the library's own V^T scratch (one per GPU). */
 #define DAN_TREE_ATTN_SCRATCH_BYTES (32LL << 20)

@@ -154,7 +154,9 @@ def test_empty_work_is_a_no_op(lib):
 
 
 def test_workspace_size(lib):
-    assert _native.workspace_size(8, 128, 640, lib) == 8 * 128 * 640 * 2
+    # fp16 V^T, then one int32 exponent per (kv head, 64-column block), rounded up to 256 bytes
+    assert _native.workspace_size(8, 128, 640, lib) == 8 * 128 * 640 * 2 + 512
+    assert _native.workspace_size(1, 64, 64, lib) == 64 * 64 * 2 + 256
     assert _native.workspace_size(8, 128, 100, lib) == 0  # not a multiple of the key tile
     assert _native.workspace_size(0, 128, 64, lib) == 0
 
@@ -163,7 +165,7 @@ def test_bad_scale_dtype_and_workspace(lib):
     x = (ctypes.c_uint8 * 4096)()
     p = (ctypes.addressof(x) + 255) // 256 * 256
     full = dict(num_work=1, q=p, k=p, v=p, out=p, segments=p, work=p, key_lo=p, col_seg=p, vt_cols=64,
-                workspace=p, workspace_bytes=8 * 128 * 64 * 2)
+                workspace=p, workspace_bytes=8 * 128 * 64 * 2 + 256)
     # non-positive, infinite and NaN scales (checked from the float's bits: the
     # library is built with -fno-honor-nans, which may fold a NaN comparison)
     for bad_scale in (0.0, -0.0, -1.0, float("inf"), float("nan"), -float("nan")):
@@ -390,3 +392,27 @@ def test_gdn_conv_argument_errors(lib, kw, status, needle):
 
 def test_gdn_conv_no_rows_is_a_no_op(lib):
     assert lib.dan_gdn_conv(ctypes.byref(_conv_args(num_out=0)), None) == _native.OK
+
+
+def test_stage_f16_checks_before_any_gpu_call(lib):
+    """dan_tree_attn_stage_f16 (fp32 q / k -> fp16 with a power-of-2 scale):
+    NULL, version, shape and alignment errors come back as status codes."""
+    x = (ctypes.c_uint8 * 4096)()
+    p = (ctypes.addressof(x) + 255) // 256 * 256
+
+    def stage(**kw):
+        a = _native.DanStageF16Args()
+        a.abi_version = _native.ABI_VERSION
+        a.d0, a.d1, a.d2 = 2, 3, 8
+        a.x, a.stride0, a.stride1, a.out, a.scale, a.partial = p, 24, 8, p, p, p
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return lib.dan_tree_attn_stage_f16(ctypes.byref(a), None)
+
+    assert lib.dan_tree_attn_stage_f16(None, None) == _native.ERR_INVALID_ARGUMENT
+    assert stage(abi_version=5) == _native.ERR_VERSION
+    assert stage(d2=6) == _native.ERR_INVALID_ARGUMENT and "multiple of 4" in _native.last_error(lib)
+    assert stage(d0=-1) == _native.ERR_INVALID_ARGUMENT
+    assert stage(scale=None) == _native.ERR_INVALID_ARGUMENT and "NULL" in _native.last_error(lib)
+    for bad in (dict(x=p + 4), dict(stride1=6), dict(out=p + 2)):
+        assert stage(**bad) == _native.ERR_INVALID_ARGUMENT and "aligned" in _native.last_error(lib)

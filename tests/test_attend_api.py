@@ -57,6 +57,6 @@ def test_custom_op_fake_output(qdt, vdt, want):
         v = torch.empty(hkv, n, d, dtype=vdt, device="cuda")
         tables = [torch.empty(8, dtype=torch.int32, device="cuda") for _ in range(7)]
         scales = [torch.empty(1, device="cuda") for _ in range(3)] if qdt == torch.float8_e4m3fn else []
-        o = torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, [1, 0, 1, 64, 128, 1, 0, 0], 0.1)
+        o = torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, [1, 0, 1, 64, 128, 1, 0, 0], 0.1, None)
         assert o.shape == (h, n, d) and o.dtype == want and o.device.type == "cuda"
         assert o.stride() == (d, h * d, 1)

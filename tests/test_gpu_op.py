@@ -27,7 +27,7 @@ def test_opcheck(gpu, cfg):
     # does not implement for float8_e4m3fn: e4m3 gets the fake-tensor check.
     utils = ("test_faketensor",) if fp8 else ("test_schema", "test_autograd_registration", "test_faketensor",
                                                "test_aot_dispatch_dynamic")
-    torch.library.opcheck(torch.ops.dan_amd.tree_attn.default, _op_args(w.q, w.k, w.v, w.segments, w.layer, None, fp8),
+    torch.library.opcheck(torch.ops.dan_amd.tree_attn.default, _op_args(w.q, w.k, w.v, w.segments, w.layer, None, fp8) + (None,),
                           test_utils=utils)
 
 
@@ -37,7 +37,7 @@ def test_compile_fullgraph(gpu):
     q, k, v, tables, scales, meta, sc = _op_args(w.q, w.k, w.v, w.segments, w.layer, None)
 
     def layer_out(q, k, v):  # the reference's o.transpose(0, 1).reshape(n, H * D)
-        return torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, meta, sc).transpose(0, 1).reshape(n, h * d)
+        return torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, meta, sc, None).transpose(0, 1).reshape(n, h * d)
 
     print(f"[gpu-case] compile c2: N={n}", flush=True)
     f = torch.compile(layer_out, fullgraph=True, backend="aot_eager")

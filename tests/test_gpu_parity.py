@@ -336,12 +336,15 @@ def test_phases_split_equals_one_call(gpu):
     """The V^T copy and the attention launched by two calls (phases 1, 2)
     give the one-call result bit for bit."""
     from dan_amd import _native
-    from dan_amd.attention import _attend_fused
+    from dan_amd.attention import _attend_fused, workspace_bytes
     w = W.config2(0, device=gpu)
     say("phases split")
     full = attend(w.q, w.k, w.v, w.segments, 0).clone()
-    _attend_fused(w.q, w.k, w.v, w.segments, 0, None, phases=_native.PHASE_PACK)
-    out = _attend_fused(w.q, w.k, w.v, w.segments, 0, None, phases=_native.PHASE_ATTEND)
+    ws = torch.empty(workspace_bytes(w.q, w.k, w.segments), dtype=torch.uint8, device=gpu)
+    _attend_fused(w.q, w.k, w.v, w.segments, 0, None, phases=_native.PHASE_PACK, workspace=ws)
+    out = _attend_fused(w.q, w.k, w.v, w.segments, 0, None, phases=_native.PHASE_ATTEND, workspace=ws)
+    with pytest.raises(ValueError, match="workspace"):
+        _attend_fused(w.q, w.k, w.v, w.segments, 0, None, phases=_native.PHASE_ATTEND)
     torch.cuda.synchronize()
     rows = torch.cat([torch.arange(s.start, s.end) for s in w.segments])
     assert torch.equal(out[:, rows], full[:, rows])
