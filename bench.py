@@ -69,12 +69,29 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
+def host_cpus():
+    """CPUs this process may run on: its affinity mask, capped by the cgroup's
+    CPU quota when one is set (a container's share of a larger machine).
+    Returns (cpus, affinity, quota or None)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, math.ceil(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(affinity, quota) if quota else affinity), affinity, quota
+
+
 def cpu_baseline(name, seed, flops, n_tokens):
-    """Oracle (reference dense path restated) on the host: 1 warm-up, median of 3."""
+    """Oracle (reference dense path restated) on the host: 1 warm-up, median of 3,
+    with one torch thread per CPU the process may use."""
     from dan_amd import workloads
     from oracle.tree_attention import attend_dense
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads, affinity, quota = host_cpus()
     torch.set_num_threads(threads)
     if name == "c5":  # e4m3 inputs: the CPU path runs on config 3's originals (same useful FLOPs)
         name = "c3"
@@ -88,8 +105,42 @@ def cpu_baseline(name, seed, flops, n_tokens):
     t = statistics.median(times)
     return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"full {name} seed {seed} workload ({n_tokens} packed tokens), fp32 torch SDPA per segment, "
-                      f"1 warm-up then median of 3 runs ({t:.3f} s); CPU: {cpu_model()}",
+                      f"1 warm-up then median of 3 runs ({t:.3f} s); {threads} threads = the process's CPUs "
+                      f"(affinity {affinity}, cgroup quota {quota if quota else 'none'}); CPU: {cpu_model()}",
             "seconds": round(t, 4), "tokens_per_s": round(n_tokens / t, 1)}
+
+
+def forward_layers(w, layers, forwards):
+    """A model forward's attention: a fresh Batch (so the tile plan is built
+    again) whose prefix entry holds one (k, v) per layer, then ``layers``
+    attend calls (each layer's prefix table built on its first call). Returns
+    ms per forward (median over ``forwards``, after one untimed forward)."""
+    from dataclasses import replace
+
+    from dan_amd.attention import Batch, attend
+
+    kw = w.attend_kwargs
+    shared = {}
+    times = []
+    for f in range(forwards + 1):
+        segs = Batch()
+        for s in w.segments:
+            past = None
+            if s.past:
+                if id(s.past) not in shared:
+                    entry = s.past[w.layer]
+                    # one prefix entry per layer: fresh tensors of the same shape (and scales)
+                    shared[id(s.past)] = {l: tuple(t.clone() for t in entry) for l in range(layers)}
+                past = shared[id(s.past)]
+            segs.append(replace(s, past=past, saved={}, _mask=None))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for layer in range(layers):
+            attend(w.q, w.k, w.v, segs, layer, **kw)
+        torch.cuda.synchronize()
+        if f:
+            times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
 
 
 def copy_calibration(mib, steps):
@@ -454,6 +505,9 @@ def main():
                     help="untimed calls of the same workload before the warm-up steps, until this much wall "
                          "time has passed: under sustained load the GPU's clock keeps ramping for about 2 s "
                          "(c3: 0.327 ms per call after 0.3 s, 0.294 ms after 2 s)")
+    ap.add_argument("--forward-layers", type=int, default=32,
+                    help="also time a model forward of this many attention layers (fresh plan, per-layer prefix "
+                         "tables; 0 skips it)")
     ap.add_argument("--front", action="store_true",
                     help="measure the attention front end (q/k norm + RoPE + layout) on --workload c3 or c4 "
                          "instead of the attention")
@@ -590,6 +644,14 @@ def main():
                      "bf16_peak_frac": round(achieved / PEAK_TFLOPS["bf16"], 4)},
         "cpu_baseline": None,
     }
+    if args.forward_layers:
+        fwd_ms = forward_layers(w, args.forward_layers, 5)
+        line["forward"] = {"layers": args.forward_layers, "ms": round(fwd_ms, 4),
+                           "ms_per_layer": round(fwd_ms / args.forward_layers, 4),
+                           "tflops": round(flops * args.forward_layers / (fwd_ms * 1e-3) / 1e12, 3),
+                           "note": "wall time of one model forward's attention layers: a fresh Batch (tile plan "
+                                   "rebuilt), one prefix entry per layer (each layer's table built on first use), "
+                                   "then the attend calls; median of 5 forwards"}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, args.seed, flops, n)
     print(json.dumps(line), flush=True)
