@@ -95,7 +95,7 @@ def cpu_baseline(name, seed, flops, n_tokens):
     torch.set_num_threads(threads)
     if name == "c5":  # e4m3 inputs: the CPU path runs on config 3's originals (same useful FLOPs)
         name = "c3"
-    w = workloads.CONFIGS[name](seed, device="cpu")
+    w = {**workloads.CONFIGS, **workloads.EXTRA}[name](seed, device="cpu")
     attend_dense(w.q, w.k, w.v, w.segments, w.layer)
     times = []
     for _ in range(3):
@@ -454,7 +454,7 @@ def bench_plan(args):
 
     lib = _native.load()
     dev = torch.device("cuda:0")
-    w = workloads.CONFIGS[args.workload](args.seed, device=dev)
+    w = {**workloads.CONFIGS, **workloads.EXTRA}[args.workload](args.seed, device=dev)
     h, hkv = w.q.shape[0], w.k.shape[0]
     tile_q, groups, cus = _native.tile_q(h, hkv, lib), _native.head_groups(h, hkv, lib), _num_cus(dev)
 
@@ -498,7 +498,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "q35"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle-ms", type=float, default=2000.0,
@@ -553,7 +553,7 @@ def main():
 
     _native.load()
     dev = torch.device("cuda:0")
-    w = workloads.CONFIGS[args.workload](args.seed, device=dev)
+    w = {**workloads.CONFIGS, **workloads.EXTRA}[args.workload](args.seed, device=dev)
     flops = useful_flops(w)
     nbytes = algorithmic_bytes(w)
     n = w.num_tokens
@@ -627,7 +627,7 @@ def main():
         "vs_baseline": None,
         "dtype": dtype,
         "data": "synthetic",
-        "config": {"workload": f"{args.workload}: " + (workloads.CONFIGS[args.workload].__doc__ or "").split(";")[0]
+        "config": {"workload": f"{args.workload}: " + ({**workloads.CONFIGS, **workloads.EXTRA}[args.workload].__doc__ or "").split(";")[0]
                    .strip().replace("\n", " "),
                    "seed": args.seed, "packed_tokens": n, "heads": f"{w.q.shape[0]}/{w.k.shape[0]}",
                    "head_dim": w.q.shape[2],

@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 KEY_TILE = 64
 SCRATCH_BYTES = 32 << 20  # DAN_TREE_ATTN_SCRATCH_BYTES: dan_tree_attn_fwd_noalloc's V^T scratch per GPU
 
@@ -176,7 +176,7 @@ def load(path=LIB_PATH):
         lib.dan_tree_attn_fwd_noalloc.restype = ctypes.c_int
         lib.dan_tree_attn_stage_f16.argtypes = [ctypes.POINTER(DanStageF16Args), _vp]
         lib.dan_tree_attn_stage_f16.restype = ctypes.c_int
-        lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32]
+        lib.dan_tree_attn_tile_q.argtypes = [_i32, _i32, _i32]
         lib.dan_tree_attn_tile_q.restype = ctypes.c_int
         lib.dan_tree_attn_head_groups.argtypes = [_i32, _i32]
         lib.dan_tree_attn_head_groups.restype = ctypes.c_int
@@ -224,9 +224,9 @@ def last_error(lib):
     return msg.decode() if msg else ""
 
 
-def tile_q(num_heads, num_kv_heads, lib=None):
+def tile_q(num_heads, num_kv_heads, head_dim=128, lib=None):
     """Queries per work item the kernel expects (0: unsupported head layout)."""
-    return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads)
+    return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads, head_dim)
 
 
 def head_groups(num_heads, num_kv_heads, lib=None):

@@ -168,8 +168,8 @@ def _check_inputs(q, k, v):
         raise ValueError(f"{h} query heads is not a multiple of {hkv} kv heads")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"q, k, v must share one of {list(_DTYPES)}; got {q.dtype}, {k.dtype}, {v.dtype}")
-    if d not in (64, 128):
-        raise ValueError(f"head_dim {d}: the gfx950 kernel is built for 64 and 128")
+    if d not in (64, 128, 256):
+        raise ValueError(f"head_dim {d}: the gfx950 kernel is built for 64, 128 and 256")
     if not (q.device == k.device == v.device):
         raise ValueError("q, k, v must be on one device")
 
@@ -325,7 +325,7 @@ def workspace_bytes(q, k, segments):
     h, n, d = q.shape
     hkv = k.shape[0]
     lib = _native.load()
-    tile_q = _native.tile_q(h, hkv, lib)
+    tile_q = _native.tile_q(h, hkv, d, lib=lib)
     groups = _native.head_groups(h, hkv, lib)
     plan = get_plan(segments, n, tile_q, q.device, groups=groups, num_cus=_num_cus(q.device))
     return _native.workspace_size(hkv, d, plan.vt_cols, lib)
@@ -345,7 +345,7 @@ def _op_args(q, k, v, segments, layer, scale, fp8_scales=None, phases=_native.PH
     lib = _native.load()
     h, n, d = q.shape
     hkv = k.shape[0]
-    tile_q = _native.tile_q(h, hkv, lib)
+    tile_q = _native.tile_q(h, hkv, d, lib=lib)
     if tile_q <= 0:
         raise ValueError(f"unsupported head layout H={h}, Hkv={hkv}")
     groups = _native.head_groups(h, hkv, lib)

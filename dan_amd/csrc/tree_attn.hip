@@ -62,9 +62,18 @@
 namespace dan {
 
 constexpr int kKeyTile = DAN_TREE_ATTN_KEY_TILE;  // keys per tile
-constexpr int kWaves = 8;                         // 2 per SIMD
-constexpr int kThreads = 64 * kWaves;
 constexpr int kWaveQ = 32;                        // queries per wave
+// Work-group shape of the attention launch by head_dim: 8 waves (2 per SIMD)
+// up to D = 128; 4 waves (1 per SIMD, each with 512 registers, O^T in
+// accumulation registers) at D = 256, whose O^T (128 registers) and Q
+// fragments (64) do not fit a wave's 256 registers next to two S tiles.
+template <int D>
+struct Shape {
+  static constexpr int waves = D == 256 ? 4 : 8;
+  static constexpr int threads = 64 * waves;
+  static constexpr int waves_per_simd = D == 256 ? 1 : 2;
+};
+inline int waves_for(int head_dim) { return head_dim == 256 ? Shape<256>::waves : Shape<128>::waves; }
 // Waves 0..kIssuers-1 (one per SIMD) issue every direct load of the stage
 // buffers; their SIMD partners only compute. The loads queue at the CU's
 // address unit; a queued wave cannot issue anything else, so the stall is
@@ -457,7 +466,10 @@ struct Lds {
   static constexpr int blocks = kBlocks + vBlocks;
   static constexpr int slots = (blocks + kIssuers - 1) / kIssuers;  // direct loads per issuing wave per tile
   static constexpr int buf = kBytes + vBytes;
-  static constexpr int nbuf = 4;
+  // Stage buffers: a ring of four where they fit (the S product of tile j+1
+  // overlaps the softmax of tile j, tile j+2 is in flight), else two (tile
+  // j+1 in flight while tile j is processed: head_dim 256).
+  static constexpr int nbuf = 4 * buf + 1024 <= 160 * 1024 ? 4 : 2;
   static constexpr int sink = nbuf * buf;
   static constexpr int total = sink + (blocks % kIssuers ? 1024 : 0);
   // Swizzle: rows per 256-byte bank period, and the width of the chunk XOR.
@@ -621,9 +633,15 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
 // e4m3. P V always runs in fp16: P keeps 11 significant bits instead of
 // bf16's 8 (or e4m3's 4), and the V^T copy is fp16.
 template <typename TQK, typename TOut, int D>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(Shape<D>::threads, Shape<D>::threads),
+                          amdgpu_waves_per_eu(Shape<D>::waves_per_simd, Shape<D>::waves_per_simd)))
 void tree_attn_kernel(const KParams args) {
   using L = Lds<D, (int)sizeof(TQK)>;
+  constexpr int NB = L::nbuf;
+  // Two stage buffers (head_dim 256): one wave per SIMD, every wave issues,
+  // and each step processes one tile while the next one loads.
+  constexpr bool kTwoStage = NB == 2;
+  static_assert(NB == 4 || (NB == 2 && Shape<D>::waves == kIssuers), "ring of 4, or 2 with every wave issuing");
   constexpr bool kF8 = std::is_same<TQK, E4M3>::value;
   constexpr int KS = QK<TQK>::step;                   // k-step of Q K^T
   constexpr int NK = D / KS;                          // k-steps of Q K^T
@@ -822,12 +840,12 @@ void tree_attn_kernel(const KParams args) {
     // Tile i of the concatenation [this unit; the next unit's first nn tiles].
     auto issue_cat = [&](int i) __attribute__((always_inline)) {
       if (i < ntile) {
-        issue(p, cur, off_b, i, (gbase + i) & 3);
+        issue(p, cur, off_b, i, (gbase + i) & (NB - 1));
       } else if (i - ntile < nn) {
         const Src nxt = make_src(p, load_scalar(p.units + u + 1));
         uint32_t off_nb[SLOTS];
         past_offsets(nxt.pk_st, off_nb);
-        issue(p, nxt, off_nb, i - ntile, (gbase + i) & 3);
+        issue(p, nxt, off_nb, i - ntile, (gbase + i) & (NB - 1));
       }
     };
     auto issued_cat = [&](int i) __attribute__((always_inline)) { return i < ntile + nn; };
@@ -1013,80 +1031,106 @@ void tree_attn_kernel(const KParams args) {
 
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
-    // Prologue: the tiles 0..2 the previous unit did not prefetch, and the
-    // next unit's tiles that fall within three of this unit's start (when this
-    // unit is shorter than three tiles), then q and key_lo. The buffers they
-    // go to held tiles that every wave finished before the previous unit's
-    // last barrier. Waiting for q (a load the compiler sees, issued last)
-    // also completes every direct load issued before it.
-    if (wave < kIssuers) {
-#pragma unroll
-      for (int t = 0; t < 3; ++t)
-        if (t >= pre && t < ntile) issue(p, cur, off_b, t, (gbase + t) & 3);
-      for (int t = ntile; t < 3; ++t) issue_cat(t);
-    }
-    if (!q_ready) load_q(p, un);
-    q_ready = false;
-    wait_vmem<0>();
-    barrier_lds();
-    f32x16 sa[2], sb[2];
-    // The running max m starts at the largest visible score of the first
-    // tile (exact, so that tile's largest p is 1). A query that sees no key
-    // of the first tile (only when the segment has neither past nor trunk)
-    // starts from m = -3e38: its p stay 0 while its keys are hidden, and its
-    // first visible key overflows the tile's row sum, which raises m to that
-    // tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0). Finite
-    // throughout, so no inf - inf.
-    qk_phase(gbase & 3, sa);
-    mask_phase(tile_of(0), sa);
-    fix_straddle(tile_of(0), sa);
-    mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
-
-    // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
-    // core, then O += V P of tile it while the VALU masks S(it+1). The last
-    // step of the unit has no next tile. Every step starts with a barrier,
-    // after which tile it+3 of the concatenation (this unit, then the next
-    // unit's first tiles) is issued into the buffer that tile it-1 used:
-    // every wave has finished tile it-1 before the barrier.
-    int it = 0;
-    auto step = [&](auto last, f32x16(&cur_s)[2], f32x16(&nxt_s)[2]) {
-      constexpr bool kLast = decltype(last)::value;
-      if (!kLast && wave < kIssuers) {
-        if (issued_cat(it + 2)) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
-        else wait_vmem<0>();
+    if constexpr (kTwoStage) {
+      // Two stage buffers: each step waits for its tile, passes the barrier
+      // (after which the other buffer, last used by the previous step, is
+      // free), issues the next tile there and processes its own: S, mask,
+      // softmax, then O += V P. The running max starts at the first tile's
+      // largest visible score, as below.
+      issue(p, cur, off_b, 0, gbase & (NB - 1));
+      load_q(p, un);
+      f32x16 s[2];
+      for (int it = 0; it < ntile; ++it) {
+        wait_vmem<0>();
+        barrier_lds();
+        const int ve = load_scalar(vexp_u + tile_of(it));
+        if (it + 1 < ntile) issue(p, cur, off_b, it + 1, (gbase + it + 1) & (NB - 1));
+        qk_phase((gbase + it) & (NB - 1), s);
+        mask_phase(tile_of(it), s);
+        fix_straddle(tile_of(it), s);
+        const float c = tile_c(tile_of(it));
+        if (it == 0) mneg = -fmaxf(s_max(s) * c, -3.0e38f);
+        const float ts = exp_phase(s, c);
+        finish_tile(s, ts, c, ve);
+        pv_phase((gbase + it) & (NB - 1));
       }
+      nn = 0;
+    } else {
+      // Prologue: the tiles 0..2 the previous unit did not prefetch, and the
+      // next unit's tiles that fall within three of this unit's start (when this
+      // unit is shorter than three tiles), then q and key_lo. The buffers they
+      // go to held tiles that every wave finished before the previous unit's
+      // last barrier. Waiting for q (a load the compiler sees, issued last)
+      // also completes every direct load issued before it.
+      if (wave < kIssuers) {
+  #pragma unroll
+        for (int t = 0; t < 3; ++t)
+          if (t >= pre && t < ntile) issue(p, cur, off_b, t, (gbase + t) & (NB - 1));
+        for (int t = ntile; t < 3; ++t) issue_cat(t);
+      }
+      if (!q_ready) load_q(p, un);
+      q_ready = false;
+      wait_vmem<0>();
       barrier_lds();
-      const int ve = load_scalar(vexp_u + tile_of(it));  // the tile's V^T exponent (finish_tile)
-      // The issuing waves load tile it+3 now (see kIssuers).
-      if (wave < kIssuers) issue_cat(it + 3);
-      if (kLast && nn > 0) {  // q and key_lo of the next unit (this unit's are no longer used)
-        load_q(p, load_scalar(p.units + u + 1));
-        q_ready = true;
+      f32x16 sa[2], sb[2];
+      // The running max m starts at the largest visible score of the first
+      // tile (exact, so that tile's largest p is 1). A query that sees no key
+      // of the first tile (only when the segment has neither past nor trunk)
+      // starts from m = -3e38: its p stay 0 while its keys are hidden, and its
+      // first visible key overflows the tile's row sum, which raises m to that
+      // tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0). Finite
+      // throughout, so no inf - inf.
+      qk_phase(gbase & (NB - 1), sa);
+      mask_phase(tile_of(0), sa);
+      fix_straddle(tile_of(0), sa);
+      mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
+
+      // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
+      // core, then O += V P of tile it while the VALU masks S(it+1). The last
+      // step of the unit has no next tile. Every step starts with a barrier,
+      // after which tile it+3 of the concatenation (this unit, then the next
+      // unit's first tiles) is issued into the buffer that tile it-1 used:
+      // every wave has finished tile it-1 before the barrier.
+      int it = 0;
+      auto step = [&](auto last, f32x16(&cur_s)[2], f32x16(&nxt_s)[2]) {
+        constexpr bool kLast = decltype(last)::value;
+        if (!kLast && wave < kIssuers) {
+          if (issued_cat(it + 2)) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
+          else wait_vmem<0>();
+        }
+        barrier_lds();
+        const int ve = load_scalar(vexp_u + tile_of(it));  // the tile's V^T exponent (finish_tile)
+        // The issuing waves load tile it+3 now (see kIssuers).
+        if (wave < kIssuers) issue_cat(it + 3);
+        if (kLast && nn > 0) {  // q and key_lo of the next unit (this unit's are no longer used)
+          load_q(p, load_scalar(p.units + u + 1));
+          q_ready = true;
+        }
+        const float c = tile_c(tile_of(it));
+        const float ts = exp_phase(cur_s, c);
+        if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), nxt_s);
+        finish_tile(cur_s, ts, c, ve);
+        pv_phase((gbase + it) & (NB - 1));
+        if (!kLast) {
+          mask_phase(tile_of(it + 1), nxt_s);
+          fix_straddle(tile_of(it + 1), nxt_s);
+        }
+        ++it;
+      };
+      using NotLast = std::integral_constant<bool, false>;
+      using Last = std::integral_constant<bool, true>;
+      for (;;) {
+        if (it + 1 >= ntile) break;
+        step(NotLast{}, sa, sb);
+        if (it + 1 >= ntile) {
+  #pragma unroll
+          for (int mb = 0; mb < 2; ++mb) sa[mb] = sb[mb];
+          break;
+        }
+        step(NotLast{}, sb, sa);
       }
-      const float c = tile_c(tile_of(it));
-      const float ts = exp_phase(cur_s, c);
-      if (!kLast) qk_phase((gbase + it + 1) & 3, nxt_s);
-      finish_tile(cur_s, ts, c, ve);
-      pv_phase((gbase + it) & 3);
-      if (!kLast) {
-        mask_phase(tile_of(it + 1), nxt_s);
-        fix_straddle(tile_of(it + 1), nxt_s);
-      }
-      ++it;
-    };
-    using NotLast = std::integral_constant<bool, false>;
-    using Last = std::integral_constant<bool, true>;
-    for (;;) {
-      if (it + 1 >= ntile) break;
-      step(NotLast{}, sa, sb);
-      if (it + 1 >= ntile) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) sa[mb] = sb[mb];
-        break;
-      }
-      step(NotLast{}, sb, sa);
+      step(Last{}, sa, sb);
     }
-    step(Last{}, sa, sb);
 
     // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
     // r4 of block db holds d = 32 db + 8 r4 + 4 hl + (0..3); lanes l and
@@ -1246,7 +1290,7 @@ hipError_t launch_attn(const KParams &kp, int grid, hipStream_t stream) {
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, kp);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(Shape<D>::threads), lds, stream, kp);
   return hipGetLastError();
 }
 
@@ -1258,9 +1302,10 @@ int dan_tree_attn_abi_version(void) { return DAN_TREE_ATTN_ABI_VERSION; }
 
 const char *dan_tree_attn_last_error(void) { return dan::g_err; }
 
-int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads) {
+int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
-  return dan::kWaveQ * dan::kWaves / dan::heads_per_group(num_heads / num_kv_heads);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
+  return dan::kWaveQ * dan::waves_for(head_dim) / dan::heads_per_group(num_heads / num_kv_heads);
 }
 
 int dan_tree_attn_head_groups(int32_t num_heads, int32_t num_kv_heads) {
@@ -1283,9 +1328,9 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   const int H = a->num_heads, Hkv = a->num_kv_heads, D = a->head_dim;
   if (H <= 0 || Hkv <= 0 || H % Hkv)
     return fail(DAN_ERR_INVALID_ARGUMENT, "num_heads %d must be a positive multiple of num_kv_heads %d", H, Hkv);
-  if (D != 64 && D != 128) return fail(DAN_ERR_UNSUPPORTED, "head_dim %d: only 64 and 128 are built", D);
+  if (D != 64 && D != 128 && D != 256) return fail(DAN_ERR_UNSUPPORTED, "head_dim %d: only 64, 128 and 256 are built", D);
   const int rep = H / Hkv;
-  const int tq = dan_tree_attn_tile_q(H, Hkv);
+  const int tq = dan_tree_attn_tile_q(H, Hkv, D);
   if (a->tile_q != tq) return fail(DAN_ERR_INVALID_ARGUMENT, "tile_q %d, the kernel needs %d", a->tile_q, tq);
   const int in = a->in_dtype, vd = a->v_dtype, out = a->out_dtype;
   const bool bf16 = in == DAN_DTYPE_BF16 && vd == DAN_DTYPE_BF16 && out == DAN_DTYPE_BF16;
@@ -1358,21 +1403,30 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   const int grid = a->num_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool d128 = D == 128;
+  // One instantiation per (input types, head_dim).
+  auto by_d = [&](auto f64, auto f128, auto f256) { return D == 64 ? f64() : D == 128 ? f128() : f256(); };
+#define DAN_PACK(TV) by_d([&] { return launch_pack<TV, 64>(pp, (int)pack_grid, s); }, \
+                          [&] { return launch_pack<TV, 128>(pp, (int)pack_grid, s); }, \
+                          [&] { return launch_pack<TV, 256>(pp, (int)pack_grid, s); })
+#define DAN_ATTN(TQK, TO) by_d([&] { return launch_attn<TQK, TO, 64>(kp, grid, s); }, \
+                               [&] { return launch_attn<TQK, TO, 128>(kp, grid, s); }, \
+                               [&] { return launch_attn<TQK, TO, 256>(kp, grid, s); })
   hipError_t err = hipSuccess;
   if (a->phases != DAN_TREE_ATTN_PHASE_ATTEND) {
-  if (bf16) err = d128 ? launch_pack<__bf16, 128>(pp, (int)pack_grid, s) : launch_pack<__bf16, 64>(pp, (int)pack_grid, s);
-  else if (f16) err = d128 ? launch_pack<_Float16, 128>(pp, (int)pack_grid, s) : launch_pack<_Float16, 64>(pp, (int)pack_grid, s);
-  else if (f8) err = d128 ? launch_pack<E4M3, 128>(pp, (int)pack_grid, s) : launch_pack<E4M3, 64>(pp, (int)pack_grid, s);
-  else err = d128 ? launch_pack<float, 128>(pp, (int)pack_grid, s) : launch_pack<float, 64>(pp, (int)pack_grid, s);
-  if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "V^T pack launch failed: %s", hipGetErrorString(err));
+    if (bf16) err = DAN_PACK(__bf16);
+    else if (f16) err = DAN_PACK(_Float16);
+    else if (f8) err = DAN_PACK(E4M3);
+    else err = DAN_PACK(float);
+    if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "V^T pack launch failed: %s", hipGetErrorString(err));
   }
   if (a->phases == DAN_TREE_ATTN_PHASE_PACK) return DAN_OK;
 
-  if (bf16) err = d128 ? launch_attn<__bf16, __bf16, 128>(kp, grid, s) : launch_attn<__bf16, __bf16, 64>(kp, grid, s);
-  else if (f16) err = d128 ? launch_attn<_Float16, _Float16, 128>(kp, grid, s) : launch_attn<_Float16, _Float16, 64>(kp, grid, s);
-  else if (f8) err = d128 ? launch_attn<E4M3, __bf16, 128>(kp, grid, s) : launch_attn<E4M3, __bf16, 64>(kp, grid, s);
-  else err = d128 ? launch_attn<_Float16, float, 128>(kp, grid, s) : launch_attn<_Float16, float, 64>(kp, grid, s);
+  if (bf16) err = DAN_ATTN(__bf16, __bf16);
+  else if (f16) err = DAN_ATTN(_Float16, _Float16);
+  else if (f8) err = DAN_ATTN(E4M3, __bf16);
+  else err = DAN_ATTN(_Float16, float);
+#undef DAN_PACK
+#undef DAN_ATTN
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "attention launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
 }

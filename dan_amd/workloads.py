@@ -248,4 +248,16 @@ def runner_shapes(seed=0, device="cpu", dtype=torch.bfloat16, head_dim=128):
                  per_segment_past=[p for _, _, p in shapes])
 
 
+def qwen35_budget(seed=0, device="cpu"):
+    """Qwen3.5's gated-attention layout (16 q / 2 kv heads, head_dim 256), bf16,
+    at config 3's structure: the 8192-token budget packed FIFO with a shared
+    1024-token prefix-cache block; q/k/v ~ N(0,1)*0.5. Not one of the five
+    configurations: it measures the head_dim 256 kernel."""
+    rng = np.random.default_rng(seed)
+    structure, used = config3_structure(rng)
+    return build("q35", structure, 16, 2, 256, torch.bfloat16, device, rng, std=0.5, past_len=1024,
+                 meta=dict(budget=BUDGET, filled=used))
+
+
 CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4, "c5": config5}
+EXTRA = {"q35": qwen35_budget}  # workloads beyond the five configurations (bench.py --workload)

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 6
+#define DAN_TREE_ATTN_ABI_VERSION 7
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -137,7 +137,7 @@ typedef struct {
   int32_t v_dtype;     /* DanDtype of v and the pasts' v: bf16, f16, f32 or e4m3 */
   int32_t num_heads;   /* H */
   int32_t num_kv_heads;/* Hkv; query head h reads kv head h / (H / Hkv) */
-  int32_t head_dim;    /* D: 64 or 128 */
+  int32_t head_dim;    /* D: 64, 128 or 256 */
   int32_t num_tokens;  /* N packed tokens */
   float scale;         /* softmax scale (1/sqrt(D) when the caller passes None) */
 
@@ -245,9 +245,11 @@ int dan_tree_attn_stage_f16(const DanStageF16Args *args, void *stream);
 int dan_tree_attn_fwd_noalloc(const DanTreeAttnArgs *args, void *stream);
 
 /* Queries per work item the kernel expects for this head configuration
- * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172).
- * Returns 0 for an unsupported configuration. */
-int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads);
+ * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172):
+ * 32 tokens per wave times the waves per query head of a work group (8
+ * waves up to head_dim 128, 4 at 256). Returns 0 for an unsupported
+ * configuration. */
+int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim);
 
 /* Head groups G of the schedule: kv heads times the query-head chunks one
  * work group covers: num_kv_heads * ceil(rep / 4), rep = num_heads /
