@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libdan_tree_attn.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 KEY_TILE = 64
 SCRATCH_BYTES = 32 << 20  # DAN_TREE_ATTN_SCRATCH_BYTES: dan_tree_attn_fwd_noalloc's V^T scratch per GPU
 
@@ -72,7 +72,7 @@ class DanTreeAttnArgs(ctypes.Structure):
                 ("tile_q", _i32), ("vt_cols", _i32),
                 ("col_seg", _vp),
                 ("workspace", _vp), ("workspace_bytes", _i64), ("phases", _i32),
-                ("units", _vp), ("sched_off", _vp), ("num_slots", _i32)]
+                ("units", _vp), ("sched_off", _vp), ("num_slots", _i32), ("counts", _vp)]
 
 
 STAGE_PARTIALS = 1024  # DAN_TREE_ATTN_STAGE_PARTIALS
@@ -104,7 +104,7 @@ class DanQkvFrontArgs(ctypes.Structure):
                 ("save_of", _vp), ("saves", _vp), ("num_saves", _i32)]
 
 
-PLAN_ABI_VERSION = 1
+PLAN_ABI_VERSION = 2
 PLAN_MAX_WORK, PLAN_MAX_SLOTS, PLAN_MAX_SEGMENTS, PLAN_MAX_BRANCHES = 4096, 256, 1024, 4096
 
 
@@ -113,7 +113,8 @@ class DanTreePlanArgs(ctypes.Structure):
                 ("num_work", _i32), ("num_cols", _i32), ("tile_q", _i32), ("groups", _i32), ("num_cus", _i32),
                 ("overhead", _i32),
                 ("segments", _vp), ("branch_starts", _vp),
-                ("key_lo", _vp), ("col_seg", _vp), ("work", _vp), ("cost", _vp), ("units", _vp), ("sched_off", _vp)]
+                ("key_lo", _vp), ("col_seg", _vp), ("work", _vp), ("cost", _vp), ("units", _vp), ("sched_off", _vp),
+                ("counts", _vp)]
 
 
 FP8_ABI_VERSION = 1

@@ -22,6 +22,7 @@ replaces the reference's three varlen flash calls plus log-sum-exp merge
 There is no CPU or fallback path: CPU tensors, a missing library or an
 unsupported shape raise.
 """
+import ctypes
 import functools
 import math
 from dataclasses import dataclass, field
@@ -259,10 +260,21 @@ def _past_table(plan, layer, hkv, d, dtype, device):
     hit = plan.past_tables.get(layer)
     if hit is not None:
         return hit
-    n = len(plan.past_dicts)
-    descs = (_native.DanPastDesc * max(n, 1))()
+    raw, refs = _past_descs(plan.past_dicts, plan.segs, layer, hkv, d, dtype, device)
+    table = raw.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else raw
+    plan.past_tables[layer] = (table, refs)
+    return plan.past_tables[layer]
+
+
+def _past_descs(past_dicts, segs, layer, hkv, d, dtype, device, capacity=None):
+    """The DanPastDesc bytes of ``layer``'s prefix-cache entries (host uint8
+    tensor, ``capacity`` entries if given) and the device tensors they point
+    at (kept alive by the caller); ``segs`` is the segment table, whose
+    past lengths are checked against the entries."""
+    n = len(past_dicts)
+    descs = (_native.DanPastDesc * max(capacity or n, 1))()
     refs = []
-    for i, past in enumerate(plan.past_dicts):
+    for i, past in enumerate(past_dicts):
         entry = past[layer]
         if dtype == E4M3:
             if len(entry) != 4:
@@ -289,13 +301,10 @@ def _past_table(plan, layer, hkv, d, dtype, device):
         descs[i].k_stride_head, descs[i].k_stride_tok = pk.stride(0), pk.stride(1)
         descs[i].v_stride_head, descs[i].v_stride_tok = pv.stride(0), pv.stride(1)
         descs[i].len = plen
-    for row in plan.segs:
+    for row in segs:
         if row[4] >= 0 and row[3] != descs[row[4]].len:
             raise ValueError(f"segment past_len {row[3]} differs from its past entry's {descs[row[4]].len} keys")
-    raw = torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8)
-    table = raw.pin_memory().to(device, non_blocking=True) if device.type == "cuda" else raw
-    plan.past_tables[layer] = (table, refs)
-    return plan.past_tables[layer]
+    return torch.frombuffer(bytearray(bytes(descs)), dtype=torch.uint8), refs
 
 
 @functools.lru_cache(maxsize=None)
@@ -384,7 +393,8 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
     fp16 or e4m3; v the same, or fp32 with fp16 q and k), rows 16-byte
     aligned; ``tables``: the plan's device tables (segments, work items,
     key_lo, col_seg), the layer's prefix-cache table and, when there is work,
-    the schedule (unit records, slot offsets); ``scales``: q, k, v scales of
+    the schedule (unit records, slot offsets) and, for a ``BudgetPlan``, the
+    batch's device counts; ``scales``: q, k, v scales of
     e4m3 inputs, or the power-of-2 q and k scales of fp32 inputs staged to fp16; ``meta``: [segments, prefix entries, work items, tile_q,
     V^T columns, slots, phases, noalloc]. Returns [H, N, D], a view of
     token-major [N, H, D] storage. The V^T copy goes to ``workspace`` when the
@@ -398,7 +408,8 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
     num_segments, num_pasts, num_work, tile_q, vt_cols, slots, phases, noalloc = meta
     out = torch.empty((n, h, d), dtype=_out_dtype(q, v), device=q.device)
     if num_work:
-        segs_d, work_d, key_lo_d, col_seg_d, past_table, units, sched_off = tables
+        segs_d, work_d, key_lo_d, col_seg_d, past_table, units, sched_off = tables[:7]
+        counts = tables[7] if len(tables) > 7 else None  # budget mode: the batch's device counts
         nbytes = _native.workspace_size(hkv, d, vt_cols, lib)
         ws = None
         if not noalloc:
@@ -431,6 +442,8 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
                 a.v_scale = scales[2].data_ptr()
         a.phases = phases
         a.units, a.sched_off, a.num_slots = units.data_ptr(), sched_off.data_ptr(), slots
+        if counts is not None:
+            a.counts = counts.data_ptr()
         launch = _native.forward_noalloc if noalloc else _native.forward
         launch(a, torch.cuda.current_stream(q.device).cuda_stream, lib)
     return out.transpose(0, 1)
@@ -440,3 +453,150 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
 def _tree_attn_fake(q, k, v, tables, scales, meta, scale, workspace):
     h, n, d = q.shape
     return q.new_empty((n, h, d), dtype=_out_dtype(q, v)).transpose(0, 1)
+
+
+class BudgetPlan:
+    """One HIP graph for changing batches under a fixed token budget.
+
+    A batch's ``TilePlan`` is sized by its own counts (work items, V^T
+    columns, slots), and those fix the launch grids. A BudgetPlan sizes its
+    tables for capacities instead -- ``num_tokens`` packed tokens in at most
+    ``max_segments`` segments with ``max_branches`` branches and
+    ``max_past_tokens`` prefix-cache tokens over all segments -- keeps them
+    at fixed device addresses, and launches with the capacities' grids. The
+    planner, the V^T copy and the attention read the batch's own counts from
+    device memory, so launches captured once serve every batch that ``load``
+    uploads afterwards (the replacement of the per-forward layout,
+    dan/attention.py:211-215, for a serving loop that replays one graph):
+
+        bp = BudgetPlan(8192, 32, 8, 128, torch.bfloat16, "cuda", max_segments=16,
+                        max_branches=256, max_past_tokens=16 * 1024)
+        bp.load(batch)                    # per batch, outside the graph: one upload, one
+                                          # planner launch, each layer's prefix table
+        out = bp.attend(q, k, v, layer)   # capturable; equals attend(q, k, v, batch, layer)
+
+    q, k, v keep their addresses between replays (copy each batch's values
+    into the captured tensors); prefix-cache entries may change freely (they
+    are reached through the prefix tables ``load`` rewrites). Rows beyond the
+    batch's segments are left as they are. ``load`` waits for its previous
+    upload to finish before reusing the host staging buffer."""
+
+    def __init__(self, num_tokens, num_heads, num_kv_heads, head_dim, dtype, device, max_segments, max_branches,
+                 max_past_tokens=0):
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("BudgetPlan runs on a gfx950 GPU only")
+        lib = _native.load()
+        self.n, self.h, self.hkv, self.d, self.dtype, self.device = num_tokens, num_heads, num_kv_heads, head_dim, dtype, device
+        self.tile_q = _native.tile_q(num_heads, num_kv_heads, head_dim, lib=lib)
+        self.groups = _native.head_groups(num_heads, num_kv_heads, lib)
+        if self.tile_q <= 0 or head_dim not in (64, 128, 256) or dtype not in _DTYPES:
+            raise ValueError(f"unsupported layout {num_heads}/{num_kv_heads} x {head_dim}, {dtype}")
+        self.max_segments, self.max_branches = max_segments, max_branches
+        self.max_work = -(-num_tokens // self.tile_q) + max_segments  # sum of ceil(n / tile_q)
+        self.max_cols = -(-(num_tokens + max_past_tokens) // _native.KEY_TILE) + max_segments
+        self.num_cus = _num_cus(device)
+        self.slots = _native.plan_slots(self.max_work, self.groups, self.num_cus, lib)
+        if (self.max_work > _native.PLAN_MAX_WORK or self.slots // self.groups > _native.PLAN_MAX_SLOTS
+                or max_segments > _native.PLAN_MAX_SEGMENTS or max_branches > _native.PLAN_MAX_BRANCHES):
+            raise ValueError(f"capacities ({self.max_work} work items, {max_segments} segments, {max_branches} branches) "
+                             "exceed the device planner's limits")
+        i32 = dict(dtype=torch.int32, device=device)
+        # counts {S, B, W, C}, the segment table, the branch starts: one upload per batch
+        size = 4 + 8 * max_segments + max(max_branches, 1)
+        self.blob = torch.zeros(size, **i32)
+        self.staging = torch.zeros(size, dtype=torch.int32).pin_memory()
+        self.counts = self.blob[:4]
+        self.segs_d = self.blob[4:4 + 8 * max_segments]
+        self.key_lo = torch.zeros(num_tokens, **i32)
+        self.col_seg = torch.zeros(self.max_cols, **i32)
+        self.work = torch.zeros((self.max_work, 8), **i32)
+        self.cost = torch.zeros(self.max_work, **i32)
+        self.units = torch.zeros((self.max_work * self.groups, 16), **i32)
+        self.sched_off = torch.zeros(self.slots + 1, **i32)
+        self.tables = {}  # layer -> (device DanPastDesc table, pinned staging)
+        self.refs = []
+        self.loaded = None
+        self._copied = torch.cuda.Event()
+        self._copied.record(torch.cuda.current_stream(device))
+
+    def _table(self, layer):
+        if layer not in self.tables:
+            nbytes = ctypes.sizeof(_native.DanPastDesc) * self.max_segments
+            self.tables[layer] = (torch.zeros(nbytes, dtype=torch.uint8, device=self.device),
+                                  torch.zeros(nbytes, dtype=torch.uint8).pin_memory())
+        return self.tables[layer][0]
+
+    def load(self, segments, layers=None):
+        """Plan ``segments`` (a Batch over this budget's tokens) on the device and
+        write the prefix tables of ``layers`` (default: every layer its
+        prefix-cache entries hold, and every layer already captured)."""
+        from .plan import device_inputs
+
+        lib = _native.load()
+        segs, starts, w, c, past_dicts = device_inputs(segments, self.n, self.tile_q)
+        if (len(segs) > self.max_segments or len(starts) > self.max_branches or w > self.max_work
+                or c > self.max_cols):
+            raise ValueError(f"batch of {len(segs)} segments, {len(starts)} branches, {w} work items, {c} V^T column "
+                             f"blocks exceeds the capacities ({self.max_segments}, {self.max_branches}, "
+                             f"{self.max_work}, {self.max_cols})")
+        stream = torch.cuda.current_stream(self.device)
+        self._copied.synchronize()  # the previous upload has left the staging buffers
+        st = self.staging.numpy()
+        st[:4] = (len(segs), len(starts), w, c)
+        st[4:4 + segs.size] = segs.ravel()
+        st[4 + 8 * self.max_segments:4 + 8 * self.max_segments + len(starts)] = starts
+        self.blob.copy_(self.staging, non_blocking=True)
+        if layers is None:
+            layers = set(self.tables)
+            if past_dicts:
+                layers |= set.intersection(*(set(pd) for pd in past_dicts))
+        refs = []
+        for layer in sorted(layers):
+            raw, r = _past_descs(past_dicts, segs, layer, self.hkv, self.d, self.dtype, self.device, self.max_segments)
+            refs += r
+            table = self._table(layer)
+            stage = self.tables[layer][1]
+            stage.copy_(raw)
+            table.copy_(stage, non_blocking=True)
+        a = _native.DanTreePlanArgs()
+        a.abi_version = _native.PLAN_ABI_VERSION
+        a.num_tokens, a.num_segments, a.num_branches = self.n, self.max_segments, self.max_branches
+        a.num_work, a.num_cols, a.tile_q, a.groups, a.num_cus, a.overhead = (self.max_work, self.max_cols, self.tile_q,
+                                                                              self.groups, self.num_cus, 1)
+        a.segments = self.segs_d.data_ptr()
+        a.branch_starts = self.blob.data_ptr() + 4 * (4 + 8 * self.max_segments)
+        a.key_lo, a.col_seg, a.work, a.cost = (self.key_lo.data_ptr(), self.col_seg.data_ptr(), self.work.data_ptr(),
+                                               self.cost.data_ptr())
+        a.units, a.sched_off, a.counts = self.units.data_ptr(), self.sched_off.data_ptr(), self.counts.data_ptr()
+        _native.plan(a, stream.cuda_stream, lib)
+        self._copied.record(stream)
+        self.refs = refs  # the prefix entries (and staged copies) the tables point at
+        self.loaded = segments
+
+    def attend(self, q, k, v, layer, scale=None, *, q_scale=None, k_scale=None, v_scale=None):
+        """``attend(q, k, v, batch, layer)`` over the batch ``load`` uploaded, with
+        the capacities' launch grids (no save side effect): safe to capture in
+        a HIP graph and replay after later ``load`` calls."""
+        if not q.is_cuda:
+            raise RuntimeError("BudgetPlan.attend runs on a gfx950 GPU only")
+        _check_inputs(q, k, v)
+        if tuple(q.shape) != (self.h, self.n, self.d) or k.shape[0] != self.hkv or q.dtype != self.dtype:
+            raise ValueError(f"q {tuple(q.shape)} {q.dtype}: this budget plan is for [{self.h}, {self.n}, {self.d}] "
+                             f"{self.dtype} with {self.hkv} kv heads")
+        if self.loaded is None:
+            raise ValueError("load a batch before attend")
+        scales = []
+        if q.dtype == E4M3:
+            scales = [_check_scale(t, nm, q.device) for t, nm in
+                      zip((q_scale, k_scale, v_scale), ("q_scale", "k_scale", "v_scale"))]
+        if q.dtype == torch.float32:
+            (q, qs), (k, ks) = _stage_f16(q), _stage_f16(k)
+            scales = [qs, ks]
+        q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+        tables = [self.segs_d, self.work, self.key_lo, self.col_seg, self._table(layer), self.units, self.sched_off,
+                  self.counts]
+        meta = [self.max_segments, self.max_segments, self.max_work, self.tile_q, self.max_cols * _native.KEY_TILE,
+                self.slots, _native.PHASES_ALL, 0]
+        softmax_scale = (1.0 / math.sqrt(self.d)) if scale is None else float(scale)
+        return torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, meta, softmax_scale, None)

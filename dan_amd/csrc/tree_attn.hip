@@ -153,6 +153,7 @@ struct PackParams {
   int32_t *vexp;  // [Hkv][vt_cols / 64]: power-of-2 exponent of each column block (V^T = V * 2^-e)
   int32_t num_kv_heads, vt_cols;
   const float *v_scale;  // e4m3 only: per-tensor scale of v (prefix-cache entries carry their own)
+  const int32_t *counts; // budget mode: device {S, B, W, C}; column blocks from C on are skipped
 };
 
 // ---------------------------------------------------------------- element I/O
@@ -553,6 +554,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t tile[D * 32];
   __shared__ float wave_max[4];
   const int kvh = blockIdx.x % p.num_kv_heads, cb = blockIdx.x / p.num_kv_heads;
+  if (p.counts && cb >= *gbl(p.counts + 3)) return;  // past this batch's columns (the grid covers the capacity)
   const DanSegmentDesc sg = load_entry(p.segs + *gbl(p.col_seg + cb));
   const int key0 = cb * kKeyTile - sg.vt_col;
   const int P = sg.past_len, PN = P + sg.n;
@@ -1389,6 +1391,7 @@ int dan_tree_attn_fwd(const DanTreeAttnArgs *a, void *stream) {
   pp.vexp = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(a->workspace) + vt_bytes(Hkv, D, a->vt_cols));
   pp.num_kv_heads = Hkv; pp.vt_cols = a->vt_cols;
   pp.v_scale = a->v_scale;
+  pp.counts = a->counts;
 
   KParams kp;
   kp.q = a->q; kp.k = a->k; kp.o = a->out; kp.vt = pp.vt; kp.vexp = pp.vexp;

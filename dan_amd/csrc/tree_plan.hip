@@ -56,6 +56,8 @@ __device__ inline T ld(const T *p) {
 
 struct Params {
   int32_t N, S, B, W, C, tile_q, G, k, overhead, max_rounds;
+  int32_t kcap;             // slots per head group the sched_off table covers (== k unless counts)
+  const int32_t *counts;    // budget mode: device {S, B, W, C} (capacities in S, B, W, C)
   const DanSegmentDesc *segs;  // LDS copies (the kernel repoints these at its own)
   const int32_t *bstart;
   int32_t *key_lo, *col_seg, *cost;
@@ -181,10 +183,20 @@ __global__ __launch_bounds__(kThreads) void plan_kernel(const Params pg) {
   Smem &sm = *reinterpret_cast<Smem *>(smem_raw);
   const int tid = threadIdx.x, lane = tid & 63;
 
-  // ---- 0. the segment table and branch starts into LDS
-  for (int i = tid; i < pg.S; i += kThreads) sm.seg[i] = ld(pg.segs + i);
-  for (int b = tid; b < pg.B; b += kThreads) sm.bst[b] = ld(pg.bstart + b);
+  // ---- 0. budget mode: this batch's counts, clamped to the capacities
   Params p = pg;
+  if (pg.counts) {
+    const DAN_GLOBAL int32_t *c = (const DAN_GLOBAL int32_t *)pg.counts;
+    p.S = min(max(c[0], 0), pg.S);
+    p.B = min(max(c[1], 0), pg.B);
+    p.W = min(max(c[2], 0), pg.W);
+    p.C = min(max(c[3], 0), pg.C);
+    p.k = max(1, min(pg.kcap, p.W));
+    p.max_rounds = 2 * p.W + 64;
+  }
+  // ---- 0. the segment table and branch starts into LDS
+  for (int i = tid; i < p.S; i += kThreads) sm.seg[i] = ld(pg.segs + i);
+  for (int b = tid; b < p.B; b += kThreads) sm.bst[b] = ld(pg.bstart + b);
   p.segs = sm.seg;
   p.bstart = sm.bst;
 
@@ -343,8 +355,8 @@ __global__ __launch_bounds__(kThreads) void plan_kernel(const Params pg) {
   }
   __syncthreads();
   const int G = p.G;
-  for (int s = tid; s <= p.k * G; s += kThreads) {
-    if (s == p.k * G) {
+  for (int s = tid; s <= p.kcap * G; s += kThreads) {
+    if (s >= p.k * G) {  // the end, and the empty slots past this batch's (budget mode)
       p.sched_off[s] = G * p.W;
     } else {
       const int j = s / G, g = s % G;
@@ -405,8 +417,9 @@ int dan_tree_attn_plan(const DanTreePlanArgs *a, void *stream) {
     return fail(DAN_ERR_INVALID_ARGUMENT, "NULL table pointer");
   dan_plan::Params p;
   p.N = a->num_tokens; p.S = a->num_segments; p.B = a->num_branches; p.W = a->num_work; p.C = a->num_cols;
-  p.tile_q = a->tile_q; p.G = a->groups; p.k = k; p.overhead = a->overhead;
+  p.tile_q = a->tile_q; p.G = a->groups; p.k = k; p.kcap = k; p.overhead = a->overhead;
   p.max_rounds = 2 * a->num_work + 64;
+  p.counts = a->counts;
   p.segs = a->segments; p.bstart = a->branch_starts;
   p.key_lo = a->key_lo; p.col_seg = a->col_seg; p.cost = a->cost; p.work = a->work;
   p.units = a->units; p.sched_off = a->sched_off;

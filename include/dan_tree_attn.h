@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_ATTN_ABI_VERSION 7
+#define DAN_TREE_ATTN_ABI_VERSION 8
 
 /* Keys per key tile; the work list's key-tile indices count in these. */
 #define DAN_TREE_ATTN_KEY_TILE 64
@@ -192,6 +192,13 @@ typedef struct {
   const DanUnit *units;
   const int32_t *sched_off; /* [num_slots + 1], sched_off[0] = 0 */
   int32_t num_slots;
+  /* Budget mode (NULL otherwise): the device int32 {S, B, W, C} a budget-mode
+   * planner launch read (dan_tree_plan.h). num_work, vt_cols and num_slots
+   * are then the capacities the tables were sized for (launch grids, the V^T
+   * copy's row stride); the V^T copy skips column blocks from C on, and the
+   * slots past this batch's are empty. The same launches, captured once,
+   * serve every batch within the capacities. */
+  const int32_t *counts;
 } DanTreeAttnArgs;
 
 #define DAN_TREE_ATTN_PHASES_ALL 0

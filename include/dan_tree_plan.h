@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define DAN_TREE_PLAN_ABI_VERSION 1
+#define DAN_TREE_PLAN_ABI_VERSION 2
 
 /* Largest work list, slot count, segment count and branch count one planner
  * launch handles (its tables, sort and schedule live in one work group's
@@ -76,6 +76,15 @@ typedef struct {
   int32_t *cost;       /* out [W] */
   DanUnit *units;      /* out [W * G] */
   int32_t *sched_off;  /* out [k * G + 1] */
+  /* Budget mode (NULL otherwise): device int32 {S, B, W, C} of this batch. The
+   * counts above are then capacities (what the tables hold; the device counts
+   * are clamped to them), the slots per head group are k = max(1, min(num_cus
+   * / G, W)) with W the device count, and sched_off has kcap * G + 1 entries
+   * for kcap = dan_tree_attn_plan_slots(capacity W, G, num_cus) / G: the
+   * slots beyond k * G are empty. So a graph captured over one batch's
+   * launches serves any batch within the capacities after one upload of its
+   * header and one planner launch. */
+  const int32_t *counts;
 } DanTreePlanArgs;
 
 /* Build the attention tables of one packed forward on the device.
