@@ -361,6 +361,13 @@ def bench_gdn(args):
     bst = ft.index_select(0, bseg)
     tr_ms = _event_ms(lambda: delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init), args.steps)
     br_ms = _event_ms(lambda: delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, bst), args.steps)
+    forms = {}  # each phase's delta rule alone (inputs gathered beforehand), in each form
+    tin = [x[trow] for x in (q, k, v, gate, beta)]
+    bin_ = [x[brow] for x in (q, k, v, gate, beta)]
+    for form in ("token", "chunk"):
+        forms[form] = {
+            "trunk_phase_ms": round(_event_ms(lambda: delta_rule(*tin, tl, init, form=form), args.steps), 4),
+            "branch_phase_ms": round(_event_ms(lambda: delta_rule(*bin_, bl, bst, form=form), args.steps), 4)}
     tokens = len(trow) + len(brow)
     flops = tokens * hv * 7 * d * d  # per token and head: decay, S^T k, the rank-1 write, S^T q
     layer = _gdn_layer_times(args, w, hk, hv, d, dev)
@@ -393,7 +400,7 @@ def bench_gdn(args):
                                f"{hk}/{hv} heads, Dk = Dv = {d}", "seed": args.seed},
         "roofline": {"bound": "fp32 VALU (sequential per run)", "achieved": round(flops / wall / 1e12, 2),
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
-                     "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4),
+                     "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4), "forms": forms,
                      "longest_run_tokens": max(tl), "us_per_token_longest_run": round(tr_ms * 1e3 / max(tl), 3)},
         "layer": layer,
         "cpu_baseline": cpu,

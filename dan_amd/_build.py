@@ -25,7 +25,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip", "gdn_conv.hip")]
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip", "gdn_chunk.hip", "gdn_conv.hip")]
 # Extra flags per source (file name -> flags).
 SRC_FLAGS = {"tree_attn.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
 INCLUDE = os.path.join(ROOT, "include")

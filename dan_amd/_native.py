@@ -126,7 +126,9 @@ class DanFp8QuantArgs(ctypes.Structure):
                 ("reserved", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
 
 
-GDN_ABI_VERSION = 2
+GDN_ABI_VERSION = 3
+GDN_FORM_TOKEN, GDN_FORM_CHUNK = 0, 1
+GDN_CHUNK = 64
 
 
 class DanGdnArgs(ctypes.Structure):
@@ -137,7 +139,7 @@ class DanGdnArgs(ctypes.Structure):
                 ("v", _vp), ("v_stride_tok", _i64), ("v_stride_head", _i64),
                 ("g", _vp), ("beta", _vp), ("states_in", _vp), ("states_out", _vp),
                 ("out", _vp), ("o_stride_tok", _i64), ("o_stride_head", _i64),
-                ("workspace", _vp), ("workspace_bytes", _i64)]
+                ("workspace", _vp), ("workspace_bytes", _i64), ("form", _i32), ("reserved", _i32)]
 
 
 class DanGdnConvArgs(ctypes.Structure):
@@ -203,7 +205,7 @@ def load(path=LIB_PATH):
         lib.dan_fp8_abi_version.restype = ctypes.c_int
         lib.dan_gdn_fwd.argtypes = [ctypes.POINTER(DanGdnArgs), _vp]
         lib.dan_gdn_fwd.restype = ctypes.c_int
-        lib.dan_gdn_workspace_size.argtypes = [_i32, _i32]
+        lib.dan_gdn_workspace_size.argtypes = [_i32, _i32, _i32, _i32, _i32, _i32]
         lib.dan_gdn_workspace_size.restype = _i64
         lib.dan_gdn_conv.argtypes = [ctypes.POINTER(DanGdnConvArgs), _vp]
         lib.dan_gdn_conv.restype = ctypes.c_int

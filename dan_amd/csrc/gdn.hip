@@ -37,6 +37,11 @@ extern thread_local char g_err[512];
 
 namespace dan_gdn {
 
+// Workspace bytes of the norm factors [N][Hk][2], rounded to 256.
+static int64_t norm_bytes(int32_t num_tokens, int32_t num_k_heads) {
+  return ((int64_t)num_tokens * num_k_heads * 2 * 4 + 255) / 256 * 256;
+}
+
 constexpr int kDk = 128;
 constexpr int kWavesPerGroup = 4;
 constexpr int kAhead = 8;  // tokens loaded ahead (the FIFO depth)
@@ -258,15 +263,36 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
   for (int i = 0; i < kRows; ++i) *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(kRows * re + i) * p.Dv) = s[i];
 }
 
+hipError_t launch_norms(const DanGdnArgs *a, float *norms, hipStream_t s) {
+  Params p{};
+  p.q = a->q; p.k = a->k; p.q_st = a->q_stride_tok; p.q_sh = a->q_stride_head;
+  p.k_st = a->k_stride_tok; p.k_sh = a->k_stride_head;
+  p.N = a->num_tokens; p.Hk = a->num_k_heads; p.norms = norms;
+  const int64_t ngrid = ((int64_t)a->num_tokens * a->num_k_heads + kWavesPerGroup - 1) / kWavesPerGroup;
+  if (ngrid == 0) return hipSuccess;
+  const dim3 block(64 * kWavesPerGroup);
+  if (a->dtype == DAN_DTYPE_BF16) hipLaunchKernelGGL(gdn_norms_kernel<__bf16>, dim3((unsigned)ngrid), block, 0, s, p);
+  else hipLaunchKernelGGL(gdn_norms_kernel<_Float16>, dim3((unsigned)ngrid), block, 0, s, p);
+  return hipGetLastError();
+}
+
 }  // namespace dan_gdn
+
+// gdn_chunk.hip: the chunked form.
+int64_t dan_gdn_chunk_record_bytes(int32_t num_tokens, int32_t num_runs, int32_t num_v_heads);
+hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *norms, float *records, hipStream_t s);
 
 extern "C" {
 
 int dan_gdn_abi_version(void) { return DAN_GDN_ABI_VERSION; }
 
-int64_t dan_gdn_workspace_size(int32_t num_tokens, int32_t num_k_heads) {
-  if (num_tokens < 0 || num_k_heads <= 0) return 0;
-  return ((int64_t)num_tokens * num_k_heads * 2 * 4 + 255) / 256 * 256;
+int64_t dan_gdn_workspace_size(int32_t form, int32_t num_tokens, int32_t num_runs, int32_t num_k_heads,
+                               int32_t num_v_heads, int32_t v_dim) {
+  if (num_tokens < 0 || num_runs < 0 || num_k_heads <= 0 || num_v_heads <= 0 || v_dim <= 0) return 0;
+  const int64_t norms = dan_gdn::norm_bytes(num_tokens, num_k_heads);
+  if (form == DAN_GDN_FORM_TOKEN) return norms;
+  if (form == DAN_GDN_FORM_CHUNK) return norms + dan_gdn_chunk_record_bytes(num_tokens, num_runs, num_v_heads);
+  return 0;
 }
 
 int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
@@ -289,9 +315,26 @@ int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
   if (((uintptr_t)a->q & 15) || ((uintptr_t)a->k & 15) || (a->q_stride_tok % 8) || (a->q_stride_head % 8) ||
       (a->k_stride_tok % 8) || (a->k_stride_head % 8))
     return fail(DAN_ERR_INVALID_ARGUMENT, "q and k rows must be 16-byte aligned");
-  if (a->workspace_bytes < dan_gdn_workspace_size(a->num_tokens, a->num_k_heads) || ((uintptr_t)a->workspace & 15))
-    return fail(DAN_ERR_INVALID_ARGUMENT, "workspace needs %lld bytes, 16-byte aligned",
-                (long long)dan_gdn_workspace_size(a->num_tokens, a->num_k_heads));
+  if (a->form != DAN_GDN_FORM_TOKEN && a->form != DAN_GDN_FORM_CHUNK) return fail(DAN_ERR_INVALID_ARGUMENT, "form %d", a->form);
+  if (a->form == DAN_GDN_FORM_CHUNK && a->v_dim % 32)
+    return fail(DAN_ERR_UNSUPPORTED, "v_dim %d: the chunked form takes a multiple of 32", a->v_dim);
+  const int64_t need =
+      dan_gdn_workspace_size(a->form, a->num_tokens, a->num_runs, a->num_k_heads, a->num_v_heads, a->v_dim);
+  if (a->workspace_bytes < need || ((uintptr_t)a->workspace & 15))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "workspace needs %lld bytes, 16-byte aligned", (long long)need);
+  if ((int64_t)a->num_tokens * a->num_k_heads > 0x7fffffffLL * dan_gdn::kWavesPerGroup)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "too many tokens x heads");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float *norms = static_cast<float *>(a->workspace);
+  if (a->form == DAN_GDN_FORM_CHUNK) {
+    if (((int64_t)a->num_runs + a->num_tokens / DAN_GDN_CHUNK) * a->num_v_heads > 0x7fffffff ||
+        ((int64_t)a->num_runs * a->num_v_heads + 7) / 8 * 8 * (a->v_dim / 32) > 0x7fffffff)
+      return fail(DAN_ERR_INVALID_ARGUMENT, "too many chunks or runs x heads");
+    float *records = reinterpret_cast<float *>(static_cast<char *>(a->workspace) + dan_gdn::norm_bytes(a->num_tokens, a->num_k_heads));
+    const hipError_t err = dan_gdn_fwd_chunked(a, norms, records, s);
+    if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "delta rule launch failed: %s", hipGetErrorString(err));
+    return DAN_OK;
+  }
   const int64_t units = (int64_t)a->num_runs * a->num_v_heads * (a->v_dim / dan_gdn::kCols);
   const int64_t grid = (units + dan_gdn::kWavesPerGroup - 1) / dan_gdn::kWavesPerGroup;
   if (grid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "too many runs x heads");
@@ -301,19 +344,14 @@ int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
   p.v_st = a->v_stride_tok; p.v_sh = a->v_stride_head; p.o_st = a->o_stride_tok; p.o_sh = a->o_stride_head;
   p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
   p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
-  p.cblocks = a->v_dim / dan_gdn::kCols; p.N = a->num_tokens; p.norms = static_cast<float *>(a->workspace);
-  const int64_t ngrid = ((int64_t)a->num_tokens * a->num_k_heads + dan_gdn::kWavesPerGroup - 1) / dan_gdn::kWavesPerGroup;
-  if (ngrid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "too many tokens x heads");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 block(64 * dan_gdn::kWavesPerGroup);
-  if (a->dtype == DAN_DTYPE_BF16) {
-    if (ngrid) hipLaunchKernelGGL(dan_gdn::gdn_norms_kernel<__bf16>, dim3((unsigned)ngrid), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdn::gdn_kernel<__bf16>, dim3((unsigned)grid), block, 0, s, p);
-  } else {
-    if (ngrid) hipLaunchKernelGGL(dan_gdn::gdn_norms_kernel<_Float16>, dim3((unsigned)ngrid), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdn::gdn_kernel<_Float16>, dim3((unsigned)grid), block, 0, s, p);
+  p.cblocks = a->v_dim / dan_gdn::kCols; p.N = a->num_tokens; p.norms = norms;
+  hipError_t err = dan_gdn::launch_norms(a, norms, s);
+  if (err == hipSuccess) {
+    const dim3 block(64 * dan_gdn::kWavesPerGroup);
+    if (a->dtype == DAN_DTYPE_BF16) hipLaunchKernelGGL(dan_gdn::gdn_kernel<__bf16>, dim3((unsigned)grid), block, 0, s, p);
+    else hipLaunchKernelGGL(dan_gdn::gdn_kernel<_Float16>, dim3((unsigned)grid), block, 0, s, p);
+    err = hipGetLastError();
   }
-  const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "delta rule launch failed: %s", hipGetErrorString(err));
   return DAN_OK;
 }

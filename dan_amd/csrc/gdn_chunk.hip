@@ -1,0 +1,388 @@
+// Gated delta rule in chunked form (gfx950): the recurrence of gdn.hip
+// (dan/models/qwen3_5.py:136-158) restated over chunks of 64 tokens, the
+// form of the reference's own CPU path (delta_rule_torch,
+// dan/models/qwen3_5.py:103-133).
+//
+// Within a chunk (rows i = 0..63 from the chunk's first token; rows past the
+// run's end are padding with g = beta = 0), with r_q, r_k the l2-norm
+// factors of q and k, G_i = g_0 + .. + g_i and gamma_i = exp(G_i):
+//   L[i][j] = beta_i r_k,i r_k,j (k_i . k_j) exp(G_i - G_j)            j < i
+//   A[i][j] = r_q,i Dk^-1/2 r_k,j (q_i . k_j) exp(G_i - G_j)           j <= i
+//   T = (I + L)^-1
+// and then, in chunk order, from the run's state S [Dk][Dv]:
+//   D = T (diag(beta) V - diag(beta gamma r_k) K S)     (the chunk's updates)
+//   O = diag(r_q Dk^-1/2 gamma) Q S + A D
+//   S <- gamma_63 S + K^T diag(exp(G_63 - G) r_k) D
+// Two launches after the norms kernel of gdn.hip:
+//   chunk_prep_kernel  every (chunk, value head) at once: K K^T and Q K^T on
+//                      v_mfma_f32_32x32x16 (exact bf16/fp16 products, fp32
+//                      sums; the norm factors and decays are applied after,
+//                      in fp32), then T by forward substitution, one column
+//                      per lane; T, A and the per-row factors go to the
+//                      chunk records of the workspace.
+//   chunk_scan_kernel  one work group per (run, value head, 32 state
+//                      columns), the state slice in LDS; the run's chunks in
+//                      order, each the five products above on
+//                      v_mfma_f32_16x16x4_f32 (fp32 operands: the state keeps
+//                      fp32 accuracy), q, k and v read in place.
+// The sequential critical path is one chunk step per 64 tokens.
+//
+// Chunk records: run r's chunks are slots r + cu[r] / 64 + j, j = 0, 1, ..;
+// r + cu[r] / 64 increases strictly with r, so the slots of different runs
+// never meet, and every slot is below num_runs + num_tokens / 64.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "dan_gdn.h"
+
+namespace dan_gdn {
+// gdn.hip: the per-token l2-norm factors, launched first by both forms.
+hipError_t launch_norms(const DanGdnArgs *a, float *norms, hipStream_t s);
+}  // namespace dan_gdn
+
+namespace dan_gdnc {
+
+constexpr int kC = DAN_GDN_CHUNK;  // tokens per chunk
+constexpr int kDk = 128;
+constexpr int kThreads = 256;
+constexpr int kCols = 32;  // state columns per scan work group
+// Floats per (slot, value head): T [64][64], A [64][64], then five rows of 64:
+// beta gamma r_k, beta, r_q Dk^-1/2 gamma, exp(G_63 - G) r_k, {gamma_63, 0, ..}.
+constexpr int kRec = 2 * kC * kC + 5 * kC;
+constexpr float kQs = 0.08838834764831845f;  // Dk^-1/2
+
+#define DAN_GLOBAL __attribute__((address_space(1)))
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+struct Params {
+  const int32_t *cu;
+  const void *q, *k, *v;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+  const float *g, *beta, *s_in, *norms;
+  float *s_out, *rec;
+  void *o;
+  int32_t Hk, Hv, Dv, R, ncb, units;
+};
+
+template <typename T>
+__device__ inline f32x16 mfma_in(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ inline f32x16 mfma_in<__bf16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f32x16 mfma_in<_Float16>(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Element `half` (0: low 16 bits) of a word holding two T.
+template <typename T>
+__device__ inline float half_of(uint32_t w, int half);
+template <>
+__device__ inline float half_of<__bf16>(uint32_t w, int half) {
+  return __builtin_bit_cast(float, half ? (w & 0xffff0000u) : (w << 16));
+}
+template <>
+__device__ inline float half_of<_Float16>(uint32_t w, int half) {
+  return (float)__builtin_bit_cast(f16x2, w)[half];
+}
+
+__device__ inline int slot_of(const int32_t *cu, int r) { return r + *(const DAN_GLOBAL int32_t *)(cu + r) / kC; }
+
+// ---------------------------------------------------------------- chunk preparation
+// Grid: slots x Hv; a slot past its run's last chunk exits at once.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
+  __shared__ float sL[kC][kC + 4];
+  __shared__ float sG[kC];
+  const int s = blockIdx.x / p.Hv, h = blockIdx.x % p.Hv;
+  int lo = 0, hi = p.R - 1;  // the run of slot s: the largest r with slot_of(r) <= s
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (slot_of(p.cu, mid) <= s) lo = mid;
+    else hi = mid - 1;
+  }
+  const int r = lo;
+  const int t0 = *(const DAN_GLOBAL int32_t *)(p.cu + r) + kC * (s - slot_of(p.cu, r));
+  const int end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
+  if (t0 >= end) return;  // the whole group, before any barrier
+  const int L = min(kC, end - t0);
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  float *rec = p.rec + ((int64_t)s * p.Hv + h) * kRec;
+  float *Tm = rec, *Am = rec + kC * kC, *vec = rec + 2 * kC * kC;
+
+  // wave 0: the gates of row `lane`, G by a prefix sum over the lanes, the row factors
+  if (wave == 0) {
+    const int i = lane;
+    const bool ok = i < L;
+    const int64_t t = t0 + min(i, L - 1);
+    float G = ok ? *(const DAN_GLOBAL float *)(p.g + t * p.Hv + h) : 0.f;
+    const float b = ok ? *(const DAN_GLOBAL float *)(p.beta + t * p.Hv + h) : 0.f;
+    const float rq = ok ? *(const DAN_GLOBAL float *)(p.norms + (t * p.Hk + hk) * 2) : 0.f;
+    const float rk = ok ? *(const DAN_GLOBAL float *)(p.norms + (t * p.Hk + hk) * 2 + 1) : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(G, off);
+      if (lane >= off) G += y;
+    }
+    const float Glast = __shfl(G, 63);  // padding rows add 0: the decay through the run's last row
+    const float gam = expf(G);
+    sG[i] = G;
+    vec[0 * kC + i] = b * gam * rk;
+    vec[1 * kC + i] = b;
+    vec[2 * kC + i] = rq * kQs * gam;
+    vec[3 * kC + i] = expf(Glast - G) * rk;
+    vec[4 * kC + i] = i == 0 ? expf(Glast) : 0.f;
+    sL[i][kC] = b * rk;  // spare columns: beta r_k, r_q Dk^-1/2 and r_k of row i
+    sL[i][kC + 1] = rq * kQs;
+    sL[i][kC + 2] = rk;
+  }
+
+  // K K^T and Q K^T, 32 x 32 block (bi, bj) per wave: lane l reads 16 bytes
+  // of row 32 b + l % 32 at element 16 kk + 8 (l / 32).
+  const int bi = wave >> 1, bj = wave & 1;
+  const int64_t ri = t0 + min(32 * bi + (lane & 31), L - 1), rj = t0 + min(32 * bj + (lane & 31), L - 1);
+  const T *ki = static_cast<const T *>(p.k) + ri * p.k_st + (int64_t)hk * p.k_sh + 8 * (lane >> 5);
+  const T *kj = static_cast<const T *>(p.k) + rj * p.k_st + (int64_t)hk * p.k_sh + 8 * (lane >> 5);
+  const T *qi = static_cast<const T *>(p.q) + ri * p.q_st + (int64_t)hk * p.q_sh + 8 * (lane >> 5);
+  f32x16 P = {}, QK = {};
+#pragma unroll
+  for (int kk = 0; kk < kDk / 16; ++kk) {
+    const u32x4 a = *(const DAN_GLOBAL u32x4 *)(ki + 16 * kk);
+    const u32x4 b = *(const DAN_GLOBAL u32x4 *)(kj + 16 * kk);
+    const u32x4 aq = *(const DAN_GLOBAL u32x4 *)(qi + 16 * kk);
+    P = mfma_in<T>(a, b, P);
+    QK = mfma_in<T>(aq, b, QK);
+  }
+  __syncthreads();  // sG and the row factors
+#pragma unroll
+  for (int rr = 0; rr < 16; ++rr) {  // accumulator: row 8 (rr / 4) + 4 (lane / 32) + rr % 4, column lane % 32
+    const int i = 32 * bi + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3), j = 32 * bj + (lane & 31);
+    const float e = (i >= j && i < L) ? expf(sG[i] - sG[j]) : 0.f;
+    const float rkj = sL[j][kC + 2];
+    sL[i][j] = i > j ? sL[i][kC] * rkj * P[rr] * e : 0.f;
+    Am[i * kC + j] = sL[i][kC + 1] * rkj * QK[rr] * e;
+  }
+  __syncthreads();
+
+  // T = (I + L)^-1 by forward substitution, column `lane` in wave 0:
+  // x_i = [i == j] - sum_{m < i} L[i][m] x_m (x_m = 0 for m < j).
+  if (wave == 0) {
+    const int j = lane;
+    float x[kC];
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      float acc = i == j ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) acc = fmaf(-sL[i][m], x[m], acc);
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < kC; ++i) Tm[i * kC + j] = x[i];
+  }
+}
+
+// ---------------------------------------------------------------- the scan over chunks
+// LDS (floats): the state slice twice (the chunk's S and the next), [128][34]
+// each; Y, D and diag(exp(G_63 - G) r_k) D, [64][36] each. With these row
+// strides every B-operand read of v_mfma_f32_16x16x4_f32 (4 rows x 16
+// columns: rows 8 apart in S, 4 apart in the others) hits 64 distinct banks.
+constexpr int kSS = 34, kSB = 36;
+constexpr int kLds = 2 * kDk * kSS + 3 * kC * kSB;
+
+__device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// Contraction orders: the 128-long sums over the state rows take k-index
+// 32 (kk / 8) + 8 q + kk % 8 at step kk in lane group q = lane / 16 (a lane's
+// q or k elements for 8 steps are 16 contiguous bytes); the 64-long sums over
+// the chunk rows take 16 (kk / 4) + 4 q + kk % 4 (4 contiguous floats of T or A).
+__device__ inline int kidx128(int kk, int q) { return 32 * (kk >> 3) + 8 * q + (kk & 7); }
+__device__ inline int kidx64(int kk, int q) { return 16 * (kk >> 2) + 4 * q + (kk & 3); }
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const Params p) {
+  __shared__ __attribute__((aligned(16))) float smem[kLds];
+  // work group b -> (unit u = r Hv + h, column block cb); the ncb groups of a
+  // unit share b % 8 and so an XCD, whose L2 then serves their common reads
+  const int b = blockIdx.x;
+  const int u = (b / (8 * p.ncb)) * 8 + (b & 7), cb = (b >> 3) % p.ncb;
+  if (u >= p.units) return;  // the whole group, before any barrier
+  const int r = u / p.Hv, h = u % p.Hv, hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, q4 = lane >> 4;
+  float *sY = smem + 2 * kDk * kSS, *sD = sY + kC * kSB, *sDs = sD + kC * kSB;
+  const int col0 = kCols * cb;
+  const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
+  for (int x = tid; x < kDk * kCols; x += kThreads)
+    smem[(x / kCols) * kSS + x % kCols] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
+  const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
+  const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
+  const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
+  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + col0;
+  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + col0;
+  const int ri = 16 * w + l16;  // the A-operand row of the 64-row products
+  int cur = 0;
+  __syncthreads();
+  for (int t0 = row0, s = r + row0 / kC; t0 < end; t0 += kC, ++s) {
+    const int L = min(kC, end - t0);
+    const float *rec = p.rec + ((int64_t)s * p.Hv + h) * kRec;
+    const float *Tm = rec, *Am = rec + kC * kC, *vec = rec + 2 * kC * kC;
+    float *sS = smem + cur * kDk * kSS, *sN = smem + (cur ^ 1) * kDk * kSS;
+
+    // operands, rows clamped to the run (padding rows carry zero factors)
+    const int64_t tr = t0 + min(ri, L - 1);
+    u32x4 ka[4], qa[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ka[j] = *(const DAN_GLOBAL u32x4 *)(kh + tr * p.k_st + 32 * j + 8 * q4);
+    const f32x4 va = *(const DAN_GLOBAL f32x4 *)(vec + 0 * kC + 16 * w + 4 * q4);
+    const f32x4 vb = *(const DAN_GLOBAL f32x4 *)(vec + 1 * kC + 16 * w + 4 * q4);
+    float vv[2][4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t t = t0 + min(16 * w + 4 * q4 + rr, L - 1);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) vv[nb][rr] = (float)*(const DAN_GLOBAL T *)(vh + t * p.v_st + 16 * nb + l16);
+    }
+    f32x4 ta[4], aa[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ta[j] = *(const DAN_GLOBAL f32x4 *)(Tm + ri * kC + 16 * j + 4 * q4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qa[j] = *(const DAN_GLOBAL u32x4 *)(qh + tr * p.q_st + 32 * j + 8 * q4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) aa[j] = *(const DAN_GLOBAL f32x4 *)(Am + ri * kC + 16 * j + 4 * q4);
+    const f32x4 vq = *(const DAN_GLOBAL f32x4 *)(vec + 2 * kC + 16 * w + 4 * q4);
+    const f32x4 vs = *(const DAN_GLOBAL f32x4 *)(vec + 3 * kC + 16 * w + 4 * q4);
+    const float glast = *(const DAN_GLOBAL float *)(vec + 4 * kC);
+    uint32_t kt[16];  // k[i][32 w + 2 l16 .. + 1] for i = kidx64(kk, q4)
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+      kt[kk] = *(const DAN_GLOBAL uint32_t *)(kh + (int64_t)(t0 + min(kidx64(kk, q4), L - 1)) * p.k_st + 32 * w + 2 * l16);
+
+    // Y = diag(beta) V - diag(beta gamma r_k) K S, rows 16 w .. 16 w + 15
+    f32x4 x[2] = {};
+#pragma unroll
+    for (int kk = 0; kk < 32; ++kk) {
+      const float a = half_of<T>(ka[kk >> 3][(kk & 7) >> 1], kk & 1);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) x[nb] = mma(a, sS[kidx128(kk, q4) * kSS + 16 * nb + l16], x[nb]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sY[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = vb[rr] * vv[nb][rr] - va[rr] * x[nb][rr];
+    __syncthreads();
+
+    // D = T Y
+    f32x4 d[2] = {};
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      const float a = ta[kk >> 2][kk & 3];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) d[nb] = mma(a, sY[kidx64(kk, q4) * kSB + 16 * nb + l16], d[nb]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        sD[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = d[nb][rr];
+        sDs[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = vs[rr] * d[nb][rr];
+      }
+    __syncthreads();
+
+    // O = diag(r_q Dk^-1/2 gamma) Q S + A D
+    f32x4 o1[2] = {}, o2[2] = {};
+#pragma unroll
+    for (int kk = 0; kk < 32; ++kk) {
+      const float a = half_of<T>(qa[kk >> 3][(kk & 7) >> 1], kk & 1);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) o1[nb] = mma(a, sS[kidx128(kk, q4) * kSS + 16 * nb + l16], o1[nb]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      const float a = aa[kk >> 2][kk & 3];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) o2[nb] = mma(a, sD[kidx64(kk, q4) * kSB + 16 * nb + l16], o2[nb]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = 16 * w + 4 * q4 + rr;
+      if (i < L) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          *(DAN_GLOBAL T *)(oh + (int64_t)(t0 + i) * p.o_st + 16 * nb + l16) = (T)(vq[rr] * o1[nb][rr] + o2[nb][rr]);
+      }
+    }
+
+    // S <- gamma_63 S + K^T diag(exp(G_63 - G) r_k) D; the wave's state rows
+    // are 32 w + 2 m + mb for row m of block mb (so one 4-byte load of k
+    // gives both blocks' A operands)
+    f32x4 sn[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sn[mb][nb][rr] = glast * sS[(32 * w + 2 * (4 * q4 + rr) + mb) * kSS + 16 * nb + l16];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const float a = half_of<T>(kt[kk], mb);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) sn[mb][nb] = mma(a, sDs[kidx64(kk, q4) * kSB + 16 * nb + l16], sn[mb][nb]);
+      }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sN[(32 * w + 2 * (4 * q4 + rr) + mb) * kSS + 16 * nb + l16] = sn[mb][nb][rr];
+    __syncthreads();  // the new state is whole, and every read of this chunk's Y, D and S is done
+    cur ^= 1;
+  }
+  const float *sS = smem + cur * kDk * kSS;
+  for (int x = tid; x < kDk * kCols; x += kThreads)
+    *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols) = sS[(x / kCols) * kSS + x % kCols];
+}
+
+int64_t slots(int32_t num_tokens, int32_t num_runs) { return (int64_t)num_runs + num_tokens / kC; }
+
+}  // namespace dan_gdnc
+
+// Bytes of chunk records that follow the norm factors in the workspace.
+int64_t dan_gdn_chunk_record_bytes(int32_t num_tokens, int32_t num_runs, int32_t num_v_heads) {
+  return dan_gdnc::slots(num_tokens, num_runs) * num_v_heads * dan_gdnc::kRec * 4;
+}
+
+// The chunked form; arguments already checked by dan_gdn_fwd, `norms` the
+// workspace's norm factors and `records` its 16-byte aligned chunk records.
+hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *norms, float *records, hipStream_t s) {
+  dan_gdnc::Params p;
+  p.cu = a->cu; p.q = a->q; p.k = a->k; p.v = a->v;
+  p.q_st = a->q_stride_tok; p.q_sh = a->q_stride_head; p.k_st = a->k_stride_tok; p.k_sh = a->k_stride_head;
+  p.v_st = a->v_stride_tok; p.v_sh = a->v_stride_head; p.o_st = a->o_stride_tok; p.o_sh = a->o_stride_head;
+  p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
+  p.norms = norms; p.rec = records;
+  p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
+  p.ncb = a->v_dim / dan_gdnc::kCols; p.units = a->num_runs * a->num_v_heads;
+  const int64_t prep = dan_gdnc::slots(a->num_tokens, a->num_runs) * a->num_v_heads;
+  const int64_t scan = ((int64_t)p.units + 7) / 8 * 8 * p.ncb;
+  hipError_t err = dan_gdn::launch_norms(a, norms, s);
+  if (err != hipSuccess) return err;
+  const dim3 block(dan_gdnc::kThreads);
+  if (a->dtype == DAN_DTYPE_BF16) {
+    if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<__bf16>, dim3((unsigned)prep), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<__bf16>, dim3((unsigned)scan), block, 0, s, p);
+  } else {
+    if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<_Float16>, dim3((unsigned)prep), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<_Float16>, dim3((unsigned)scan), block, 0, s, p);
+  }
+  return hipGetLastError();
+}

@@ -30,12 +30,23 @@ def _row_ok(t):
     return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * t.element_size()) % 16 == 0 for s in t.stride()[:-1])
 
 
-def delta_rule(q, k, v, g, beta, lengths, states, cu=None):
+# Runs at least this long go through the chunked form (when Dv is a multiple
+# of 32): below it the token form's per-token step is cheaper than the chunked
+# form's fixed cost per launch.
+CHUNK_MIN_RUN = 128
+
+
+def delta_rule(q, k, v, g, beta, lengths, states, cu=None, form=None):
     """q, k [N, Hk, 128]; v [N, Hv, Dv] (bf16 or fp16, CUDA); g, beta [N, Hv];
     ``lengths``: run lengths summing to N (runs are consecutive rows);
     ``states`` [R, Hv, 128, Dv] fp32. Returns (out [N, Hv, Dv] in q's dtype,
     final states [R, Hv, 128, Dv] fp32). ``cu``: optional precomputed
-    (device, host) cumulative lengths, as dan passes them."""
+    (device, host) cumulative lengths, as dan passes them. ``form``: "token"
+    (token by token: a run's results do not depend on how it is split into
+    calls), "chunk" (64 tokens per step on the matrix cores, Dv a multiple of
+    32), or None to take "chunk" when the longest run has at least
+    CHUNK_MIN_RUN tokens and Dv allows it. Both forms compute the same
+    recurrence in fp32."""
     if not q.is_cuda:
         raise RuntimeError("dan_amd.deltanet.delta_rule runs on a gfx950 GPU only; got tensors on "
                            f"{q.device} (the CPU forms are the test oracle, not a backend)")
@@ -50,6 +61,11 @@ def delta_rule(q, k, v, g, beta, lengths, states, cu=None):
         raise ValueError(f"run lengths {list(lengths)[:8]}... must be >= 0 and sum to {n}")
     if tuple(states.shape) != (r, hv, dk, dv):
         raise ValueError(f"states {tuple(states.shape)}: want {(r, hv, dk, dv)}")
+    if form is None:
+        form = "chunk" if dv % 32 == 0 and max(lengths, default=0) >= CHUNK_MIN_RUN else "token"
+    if form not in ("token", "chunk"):
+        raise ValueError(f"form {form!r}: 'token', 'chunk' or None")
+    code = _native.GDN_FORM_CHUNK if form == "chunk" else _native.GDN_FORM_TOKEN
     dev = q.device
     # a fresh copy when rows are misaligned (contiguous() keeps a misaligned base)
     q = q if _row_ok(q) else torch.empty_like(q, memory_format=torch.contiguous_format).copy_(q)
@@ -77,9 +93,9 @@ def delta_rule(q, k, v, g, beta, lengths, states, cu=None):
     a.g, a.beta = g.data_ptr(), beta.data_ptr()
     a.states_in, a.states_out = s_in.data_ptr(), finals.data_ptr()
     a.out, a.o_stride_tok, a.o_stride_head = out.data_ptr(), out.stride(0), out.stride(1)
-    nbytes = _native.load().dan_gdn_workspace_size(n, hk)
+    nbytes = _native.load().dan_gdn_workspace_size(code, n, r, hk, hv, dv)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    a.workspace, a.workspace_bytes, a.form = ws.data_ptr(), nbytes, code
     _native.gdn(a, torch.cuda.current_stream(dev).cuda_stream)
     return out, finals
 

@@ -29,7 +29,18 @@
 extern "C" {
 #endif
 
-#define DAN_GDN_ABI_VERSION 2
+#define DAN_GDN_ABI_VERSION 3
+
+/* Tokens per chunk of the chunked form. */
+#define DAN_GDN_CHUNK 64
+
+/* How dan_gdn_fwd walks a run. Both give the same recurrence within fp32
+ * rounding: the token form steps token by token (a run's results do not
+ * depend on how a caller splits it into calls); the chunked form steps 64
+ * tokens at a time on the matrix cores, the form of the reference's own
+ * CPU path (dan/models/qwen3_5.py:103-133, delta_rule_torch), and is the
+ * faster one once runs are longer than a few chunks. */
+typedef enum { DAN_GDN_FORM_TOKEN = 0, DAN_GDN_FORM_CHUNK = 1 } DanGdnForm;
 
 typedef struct {
   int32_t abi_version; /* DAN_GDN_ABI_VERSION */
@@ -37,7 +48,7 @@ typedef struct {
   int32_t num_k_heads; /* Hk */
   int32_t num_v_heads; /* Hv, a multiple of Hk */
   int32_t k_dim;       /* Dk: 128 */
-  int32_t v_dim;       /* Dv: a multiple of 8, at most 256 */
+  int32_t v_dim;       /* Dv: a multiple of 8 (of 32 for the chunked form), at most 256 */
   int32_t num_runs;    /* R */
   int32_t num_tokens;  /* N */
   /* Run r covers packed rows cu[r] .. cu[r + 1] - 1 (cu[0] = 0, non-decreasing). */
@@ -50,9 +61,12 @@ typedef struct {
   const float *states_in; /* [R, Hv, Dk, Dv] */
   float *states_out;      /* [R, Hv, Dk, Dv] (may equal states_in) */
   void *out; int64_t o_stride_tok, o_stride_head; /* [N, Hv, Dv] */
-  /* Device scratch of at least dan_gdn_workspace_size(N, Hk) bytes, 16-byte
-   * aligned: the per-token l2-norm factors of q and k. */
+  /* Device scratch of at least dan_gdn_workspace_size(form, N, R, Hk, Hv, Dv)
+   * bytes, 16-byte aligned: the per-token l2-norm factors of q and k, and
+   * for the chunked form each chunk's triangular factors. */
   void *workspace; int64_t workspace_bytes;
+  int32_t form;     /* DanGdnForm */
+  int32_t reserved; /* 0 */
 } DanGdnArgs;
 
 /* The gated delta rule over every run, from states_in to states_out.
@@ -60,7 +74,10 @@ typedef struct {
  * recurrent kernel, or delta_rule_torch) on gfx950. */
 int dan_gdn_fwd(const DanGdnArgs *args, void *stream);
 
-int64_t dan_gdn_workspace_size(int32_t num_tokens, int32_t num_k_heads);
+/* Workspace bytes for dan_gdn_fwd; 0 for arguments it would reject. The
+ * chunked form's part grows as (R + N / 64) Hv 34 KiB. */
+int64_t dan_gdn_workspace_size(int32_t form, int32_t num_tokens, int32_t num_runs, int32_t num_k_heads,
+                               int32_t num_v_heads, int32_t v_dim);
 
 /* The input side of one DeltaNet phase, dan/models/qwen3_5.py:212-220
  * (DeltaNet._phase up to the delta rule) with the gates of

@@ -366,6 +366,35 @@ def test_gdn_argument_errors(lib, kw, status, needle):
     assert needle in _native.last_error(lib)
 
 
+def _gdn_ptrs(**kw):
+    # non-NULL, 16-byte aligned stand-ins: every case below fails its check before any launch
+    ptrs = {f: 4096 for f in ("cu", "q", "k", "v", "g", "beta", "states_in", "states_out", "out", "workspace")}
+    return _gdn_args(num_tokens=128, q_stride_tok=256, q_stride_head=128, k_stride_tok=256, k_stride_head=128,
+                     **{**ptrs, **kw})
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(form=2), _native.ERR_INVALID_ARGUMENT, "form"),
+    (dict(form=_native.GDN_FORM_CHUNK, v_dim=40), _native.ERR_UNSUPPORTED, "multiple of 32"),
+    (dict(form=_native.GDN_FORM_CHUNK, workspace_bytes=2048), _native.ERR_INVALID_ARGUMENT, "workspace needs"),
+    (dict(form=_native.GDN_FORM_TOKEN, workspace_bytes=1024), _native.ERR_INVALID_ARGUMENT, "workspace needs"),
+])
+def test_gdn_form_and_workspace_errors(lib, kw, status, needle):
+    rc = lib.dan_gdn_fwd(ctypes.byref(_gdn_ptrs(**kw)), None)
+    assert rc == status
+    assert needle in _native.last_error(lib)
+
+
+def test_gdn_workspace_size(lib):
+    norms = (1000 * 2 * 2 * 4 + 255) // 256 * 256
+    assert lib.dan_gdn_workspace_size(_native.GDN_FORM_TOKEN, 1000, 3, 2, 4, 128) == norms
+    # chunk records: (runs + tokens // 64) slots x value heads x (T, A: 64 x 64 each, five rows of 64) floats
+    rec = (3 + 1000 // 64) * 4 * (2 * 64 * 64 + 5 * 64) * 4
+    assert lib.dan_gdn_workspace_size(_native.GDN_FORM_CHUNK, 1000, 3, 2, 4, 128) == norms + rec
+    assert lib.dan_gdn_workspace_size(7, 1000, 3, 2, 4, 128) == 0
+    assert lib.dan_gdn_workspace_size(_native.GDN_FORM_CHUNK, -1, 3, 2, 4, 128) == 0
+
+
 def test_gdn_no_runs_is_a_no_op(lib):
     assert lib.dan_gdn_fwd(ctypes.byref(_gdn_args(num_runs=0)), None) == _native.OK
     assert lib.dan_gdn_abi_version() == _native.GDN_ABI_VERSION

@@ -5,11 +5,13 @@ CPU tests pin against the restated chunked form and closed forms.
 Bars (fp32 state, outputs rounded to the model dtype):
 - outputs within 2^-8 of |reference| + 2e-3 (bf16; 2^-11 and 5e-4 for fp16);
 - final states within 1e-4 + 1e-4 |reference|;
-- splitting a run into two calls, the second from the first's final state,
-  is bit-identical to one call (the kernel's arithmetic per token does not
-  depend on where a run starts);
+- token form: splitting a run into two calls, the second from the first's
+  final state, is bit-identical to one call (the kernel's arithmetic per
+  token does not depend on where a run starts); chunked form: the split
+  moves the chunk boundaries, and both results stay within the bars above;
 - the tree phases (trunk part 1, part 2 from its states, branches from the
   trunk's final state) equal the oracle run over each root-to-leaf path."""
+import functools
 import sys
 
 import numpy as np
@@ -48,13 +50,14 @@ def check(out, fin, ref_o, ref_f, dtype):
     assert (ef <= 1e-4 + 1e-4 * ref_f.double().abs()).all()
 
 
+@pytest.mark.parametrize("form", ["token", "chunk"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("hk,hv,dv", [(2, 2, 128), (2, 4, 128), (1, 3, 64)])
-def test_delta_rule_matches_oracle(gpu, dtype, hk, hv, dv):
-    lengths = [5, 0, 1, 300, 64, 17]
-    say(f"delta rule {dtype} Hk {hk} Hv {hv} Dv {dv} runs {lengths}")
+@pytest.mark.parametrize("hk,hv,dv", [(2, 2, 128), (2, 4, 128), (1, 3, 64), (1, 2, 256)])
+def test_delta_rule_matches_oracle(gpu, form, dtype, hk, hv, dv):
+    lengths = [5, 0, 1, 300, 64, 17, 129]
+    say(f"delta rule {form} {dtype} Hk {hk} Hv {hv} Dv {dv} runs {lengths}")
     q, k, v, g, b, st = inputs(lengths, hk, hv, dv, dtype, gpu, seed=hk * 10 + hv + dv)
-    out, fin = delta_rule(q, k, v, g, b, lengths, st)
+    out, fin = delta_rule(q, k, v, g, b, lengths, st, form=form)
     torch.cuda.synchronize()
     ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), lengths, st.cpu(), recurrent=True)
     check(out, fin, ref_o, ref_f, dtype)
@@ -62,13 +65,38 @@ def test_delta_rule_matches_oracle(gpu, dtype, hk, hv, dv):
 
 
 def test_split_run_is_bit_identical(gpu):
-    say("delta rule: one run of 400 tokens vs two calls (150 + 250)")
+    say("delta rule, token form: one run of 400 tokens vs two calls (150 + 250)")
     q, k, v, g, b, st = inputs([400], 2, 2, 128, torch.bfloat16, gpu, seed=1)
-    out, fin = delta_rule(q, k, v, g, b, [400], st)
-    o1, f1 = delta_rule(q[:150], k[:150], v[:150], g[:150], b[:150], [150], st)
-    o2, f2 = delta_rule(q[150:], k[150:], v[150:], g[150:], b[150:], [250], f1)
+    out, fin = delta_rule(q, k, v, g, b, [400], st, form="token")
+    o1, f1 = delta_rule(q[:150], k[:150], v[:150], g[:150], b[:150], [150], st, form="token")
+    o2, f2 = delta_rule(q[150:], k[150:], v[150:], g[150:], b[150:], [250], f1, form="token")
     torch.cuda.synchronize()
     assert torch.equal(torch.cat([o1, o2]), out) and torch.equal(f2, fin)
+
+
+def test_chunk_form_split_run(gpu):
+    say("delta rule, chunked form: one run of 400 tokens vs two calls (150 + 250)")
+    q, k, v, g, b, st = inputs([400], 2, 2, 128, torch.bfloat16, gpu, seed=1)
+    out, fin = delta_rule(q, k, v, g, b, [400], st, form="chunk")
+    o1, f1 = delta_rule(q[:150], k[:150], v[:150], g[:150], b[:150], [150], st, form="chunk")
+    o2, f2 = delta_rule(q[150:], k[150:], v[150:], g[150:], b[150:], [250], f1, form="chunk")
+    torch.cuda.synchronize()
+    ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), [400], st.cpu(), recurrent=True)
+    check(out, fin, ref_o, ref_f, torch.bfloat16)
+    check(torch.cat([o1, o2]), f2, ref_o, ref_f, torch.bfloat16)
+
+
+@pytest.mark.parametrize("form", ["token", "chunk"])
+def test_strong_decay(gpu, form):
+    """Gates down to -8 per token: within a chunk exp(G) underflows to 0 and
+    the state forgets; both forms follow the recurrence."""
+    say(f"delta rule {form}: strong decay")
+    q, k, v, g, b, st = inputs([3, 250], 1, 2, 128, torch.bfloat16, gpu, seed=7)
+    g = g * 25.0
+    out, fin = delta_rule(q, k, v, g, b, [3, 250], st, form=form)
+    torch.cuda.synchronize()
+    ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), [3, 250], st.cpu(), recurrent=True)
+    check(out, fin, ref_o, ref_f, torch.bfloat16)
 
 
 def test_tree_phases_equal_paths(gpu):
@@ -102,20 +130,22 @@ def test_errors(gpu):
         delta_rule(q, k, v, g, b, [3], st)
     with pytest.raises(ValueError):
         delta_rule(q.float(), k.float(), v.float(), g, b, [4], st)
+    with pytest.raises(ValueError):
+        delta_rule(q, k, v, g, b, [4], st, form="chunked")
+    q2, k2, v2, g2, b2, st2 = inputs([4], 1, 1, 40, torch.bfloat16, gpu, seed=0)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        delta_rule(q2, k2, v2, g2, b2, [4], st2, form="chunk")
 
 
-def test_c3_tree_phases_match_oracle(gpu):
-    """The c3 tree at full size (5 trunks up to 1843 tokens, 45 branches,
-    8192 tokens, 16/16 heads of 128): the trunk phase from random states,
-    then the branch phase from the trunk finals, against the oracle's
-    float64 token recurrence on the same inputs, with the bf16 bars of the
-    small cases."""
+@functools.lru_cache(maxsize=1)
+def _c3_case():
+    """The c3 tree's DeltaNet inputs (CPU) and the oracle's float64 token
+    recurrence over them: trunk phase, then branch phase from its finals."""
     from dan_amd import workloads
 
     w = workloads.config3(0, device="cpu")
     trunks = [(s.start, s.trunk) for s in w.segments]
     branches = [(a, b - a, i) for i, s in enumerate(w.segments) for a, b in s.branches]
-    say(f"delta rule c3: {len(trunks)} trunks (longest {max(t for _, t in trunks)}), {len(branches)} branches")
     g = torch.Generator().manual_seed(21)
     n, h, d = w.num_tokens, 16, 128
     q = torch.randn(n, h, d, generator=g).bfloat16()
@@ -128,12 +158,25 @@ def test_c3_tree_phases_match_oracle(gpu):
     brow = torch.cat([torch.arange(a, a + m) for a, m, _ in branches])
     bseg = torch.tensor([i for _, _, i in branches])
     tl, bl = [t for _, t in trunks], [m for _, m, _ in branches]
-    dv = [x.to(gpu) for x in (q, k, v, gg, b)]
-    ot, ft = delta_rule(*(x[trow.to(gpu)] for x in dv), tl, init.to(gpu))
-    ob, fb = delta_rule(*(x[brow.to(gpu)] for x in dv), bl, ft.index_select(0, bseg.to(gpu)))
-    torch.cuda.synchronize()
     torch.set_num_threads(8)
-    rt_o, rt_f = OD.delta_rule(*(x[trow] for x in (q, k, v, gg, b)), tl, init, recurrent=True)
+    rt = OD.delta_rule(*(x[trow] for x in (q, k, v, gg, b)), tl, init, recurrent=True)
+    rb = OD.delta_rule(*(x[brow] for x in (q, k, v, gg, b)), bl, rt[1].index_select(0, bseg), recurrent=True)
+    return (q, k, v, gg, b), init, trow, brow, bseg, tl, bl, rt, rb
+
+
+@pytest.mark.parametrize("form", ["token", "chunk"])
+def test_c3_tree_phases_match_oracle(gpu, form):
+    """The c3 tree at full size (5 trunks up to 1843 tokens, 45 branches,
+    8192 tokens, 16/16 heads of 128): the trunk phase from random states,
+    then the branch phase from the trunk finals, against the oracle's
+    float64 token recurrence on the same inputs, with the bf16 bars of the
+    small cases."""
+    say(f"delta rule c3 ({form}): oracle")
+    x, init, trow, brow, bseg, tl, bl, (rt_o, rt_f), (rb_o, rb_f) = _c3_case()
+    say(f"delta rule c3 ({form}): {len(tl)} trunks (longest {max(tl)}), {len(bl)} branches")
+    dv = [t.to(gpu) for t in x]
+    ot, ft = delta_rule(*(t[trow.to(gpu)] for t in dv), tl, init.to(gpu), form=form)
+    ob, fb = delta_rule(*(t[brow.to(gpu)] for t in dv), bl, ft.index_select(0, bseg.to(gpu)), form=form)
+    torch.cuda.synchronize()
     check(ot, ft, rt_o, rt_f, torch.bfloat16)
-    rb_o, rb_f = OD.delta_rule(*(x[brow] for x in (q, k, v, gg, b)), bl, rt_f.index_select(0, bseg), recurrent=True)
     check(ob, fb, rb_o, rb_f, torch.bfloat16)
