@@ -398,7 +398,9 @@ def bench_gdn(args):
         "dtype": "fp32 state, bf16 io", "data": "synthetic",
         "config": {"workload": f"gdn-c3: {len(trunks)} trunks (longest {max(tl)}), {len(bl)} branches, {tokens} tokens, "
                                f"{hk}/{hv} heads, Dk = Dv = {d}", "seed": args.seed},
-        "roofline": {"bound": "fp32 VALU (sequential per run)", "achieved": round(flops / wall / 1e12, 2),
+        "roofline": {"bound": "fp32 MFMA, sequential in chunks of 64 tokens per run (trunks in the chunked form; "
+                              "branches shorter than deltanet.CHUNK_MIN_RUN token by token on the VALU)",
+                     "achieved": round(flops / wall / 1e12, 2),
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
                      "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4), "forms": forms,
                      "longest_run_tokens": max(tl), "us_per_token_longest_run": round(tr_ms * 1e3 / max(tl), 3)},

@@ -280,7 +280,7 @@ hipError_t launch_norms(const DanGdnArgs *a, float *norms, hipStream_t s) {
 
 // gdn_chunk.hip: the chunked form.
 int64_t dan_gdn_chunk_record_bytes(int32_t num_tokens, int32_t num_runs, int32_t num_v_heads);
-hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *norms, float *records, hipStream_t s);
+hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t s);
 
 extern "C" {
 
@@ -291,7 +291,7 @@ int64_t dan_gdn_workspace_size(int32_t form, int32_t num_tokens, int32_t num_run
   if (num_tokens < 0 || num_runs < 0 || num_k_heads <= 0 || num_v_heads <= 0 || v_dim <= 0) return 0;
   const int64_t norms = dan_gdn::norm_bytes(num_tokens, num_k_heads);
   if (form == DAN_GDN_FORM_TOKEN) return norms;
-  if (form == DAN_GDN_FORM_CHUNK) return norms + dan_gdn_chunk_record_bytes(num_tokens, num_runs, num_v_heads);
+  if (form == DAN_GDN_FORM_CHUNK) return dan_gdn_chunk_record_bytes(num_tokens, num_runs, num_v_heads);
   return 0;
 }
 
@@ -330,8 +330,7 @@ int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
     if (((int64_t)a->num_runs + a->num_tokens / DAN_GDN_CHUNK) * a->num_v_heads > 0x7fffffff ||
         ((int64_t)a->num_runs * a->num_v_heads + 7) / 8 * 8 * (a->v_dim / 32) > 0x7fffffff)
       return fail(DAN_ERR_INVALID_ARGUMENT, "too many chunks or runs x heads");
-    float *records = reinterpret_cast<float *>(static_cast<char *>(a->workspace) + dan_gdn::norm_bytes(a->num_tokens, a->num_k_heads));
-    const hipError_t err = dan_gdn_fwd_chunked(a, norms, records, s);
+    const hipError_t err = dan_gdn_fwd_chunked(a, static_cast<float *>(a->workspace), s);
     if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "delta rule launch failed: %s", hipGetErrorString(err));
     return DAN_OK;
   }

@@ -13,12 +13,13 @@
 //   D = T (diag(beta) V - diag(beta gamma r_k) K S)     (the chunk's updates)
 //   O = diag(r_q Dk^-1/2 gamma) Q S + A D
 //   S <- gamma_63 S + K^T diag(exp(G_63 - G) r_k) D
-// Two launches after the norms kernel of gdn.hip:
-//   chunk_prep_kernel  every (chunk, value head) at once: K K^T and Q K^T on
+// Two launches:
+//   chunk_prep_kernel  every (chunk, value head) at once: the l2-norm factors
+//                      of the chunk's q and k rows, K K^T and Q K^T on
 //                      v_mfma_f32_32x32x16 (exact bf16/fp16 products, fp32
 //                      sums; the norm factors and decays are applied after,
 //                      in fp32), then T by forward substitution, one column
-//                      per lane; T, A and the per-row factors go to the
+//                      per four lanes; T, A and the per-row factors go to the
 //                      chunk records of the workspace.
 //   chunk_scan_kernel  one work group per (run, value head, 32 state
 //                      columns), the state slice in LDS; the run's chunks in
@@ -35,11 +36,6 @@
 #include <stdint.h>
 
 #include "dan_gdn.h"
-
-namespace dan_gdn {
-// gdn.hip: the per-token l2-norm factors, launched first by both forms.
-hipError_t launch_norms(const DanGdnArgs *a, float *norms, hipStream_t s);
-}  // namespace dan_gdn
 
 namespace dan_gdnc {
 
@@ -65,7 +61,7 @@ struct Params {
   const int32_t *cu;
   const void *q, *k, *v;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
-  const float *g, *beta, *s_in, *norms;
+  const float *g, *beta, *s_in;
   float *s_out, *rec;
   void *o;
   int32_t Hk, Hv, Dv, R, ncb, units;
@@ -92,6 +88,18 @@ __device__ inline float half_of<__bf16>(uint32_t w, int half) {
 template <>
 __device__ inline float half_of<_Float16>(uint32_t w, int half) {
   return (float)__builtin_bit_cast(f16x2, w)[half];
+}
+
+// Sum of squares of the 8 T in x, in fp32.
+template <typename T>
+__device__ inline float sumsq8(u32x4 x) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float y = half_of<T>(x[e >> 1], e & 1);
+    s = fmaf(y, y, s);
+  }
+  return s;
 }
 
 __device__ inline int slot_of(const int32_t *cu, int r) { return r + *(const DAN_GLOBAL int32_t *)(cu + r) / kC; }
@@ -126,8 +134,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
     const int64_t t = t0 + min(i, L - 1);
     float G = ok ? *(const DAN_GLOBAL float *)(p.g + t * p.Hv + h) : 0.f;
     const float b = ok ? *(const DAN_GLOBAL float *)(p.beta + t * p.Hv + h) : 0.f;
-    const float rq = ok ? *(const DAN_GLOBAL float *)(p.norms + (t * p.Hk + hk) * 2) : 0.f;
-    const float rk = ok ? *(const DAN_GLOBAL float *)(p.norms + (t * p.Hk + hk) * 2 + 1) : 0.f;
+    // 1 / sqrt(sum x^2 + 1e-6) of row t of q and of k (dan/models/qwen3_5.py:99-100)
+    const T *qr = static_cast<const T *>(p.q) + t * p.q_st + (int64_t)hk * p.q_sh;
+    const T *kr = static_cast<const T *>(p.k) + t * p.k_st + (int64_t)hk * p.k_sh;
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int j = 0; j < kDk / 8; ++j) {
+      sq += sumsq8<T>(*(const DAN_GLOBAL u32x4 *)(qr + 8 * j));
+      sk += sumsq8<T>(*(const DAN_GLOBAL u32x4 *)(kr + 8 * j));
+    }
+    const float rq = ok ? 1.0f / sqrtf(sq + 1e-6f) : 0.f;
+    const float rk = ok ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float y = __shfl_up(G, off);
@@ -173,20 +190,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
   }
   __syncthreads();
 
-  // T = (I + L)^-1 by forward substitution, column `lane` in wave 0:
-  // x_i = [i == j] - sum_{m < i} L[i][m] x_m (x_m = 0 for m < j).
-  if (wave == 0) {
-    const int j = lane;
-    float x[kC];
+  // T = (I + L)^-1 by forward substitution, x_i = [i == j] - sum_{m < i} L[i][m] x_m
+  // for column j: wave w solves columns 16 w .. 16 w + 15, four lanes per
+  // column (lane 4 c + p: column 16 w + c, the terms m = p mod 4), the four
+  // partial sums added by two quad swaps. Rows above 16 w are 0 in these
+  // columns; L[i][m] = 0 for m >= i, so whole groups of four are summed.
+  {
+    const int j = 16 * wave + (lane >> 2), part = lane & 3;
+    float xm[kC / 4];  // x_{4 k + part}
+#pragma unroll
+    for (int k = 0; k < kC / 4; ++k) xm[k] = 0.f;
 #pragma unroll
     for (int i = 0; i < kC; ++i) {
-      float acc = i == j ? 1.f : 0.f;
+      if (i >= 16 * wave) {  // wave-uniform
+        float acc = 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(-sL[i][m], x[m], acc);
-      x[i] = acc;
+        for (int k = 0; k < (i + 3) / 4; ++k) acc = fmaf(sL[i][4 * k + part], xm[k], acc);
+        acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0xB1, 0xf, 0xf, false));
+        acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x4E, 0xf, 0xf, false));
+        const float xi = (i == j ? 1.f : 0.f) - acc;
+        if (part == (i & 3)) xm[i >> 2] = xi;
+      }
     }
 #pragma unroll
-    for (int i = 0; i < kC; ++i) Tm[i * kC + j] = x[i];
+    for (int k = 0; k < kC / 4; ++k) Tm[(4 * k + part) * kC + j] = xm[k];
   }
 }
 
@@ -197,18 +224,48 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
 // columns: rows 8 apart in S, 4 apart in the others) hits 64 distinct banks.
 constexpr int kSS = 34, kSB = 36;
 constexpr int kLds = 2 * kDk * kSS + 3 * kC * kSB;
+constexpr int kScanThreads = 512;  // 8 waves: 4 row blocks x 2 column halves of the slice
 
 __device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+// A work-group barrier that waits for this wave's LDS operations only:
+// __syncthreads() also waits for every global load in flight, which would
+// drain the next chunk's operand loads at each of the chunk's barriers.
+__device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Contraction orders: the 128-long sums over the state rows take k-index
 // 32 (kk / 8) + 8 q + kk % 8 at step kk in lane group q = lane / 16 (a lane's
 // q or k elements for 8 steps are 16 contiguous bytes); the 64-long sums over
-// the chunk rows take 16 (kk / 4) + 4 q + kk % 4 (4 contiguous floats of T or A).
+// the chunk rows take 16 (kk / 4) + 4 q + kk % 4 (4 contiguous floats of T or
+// A), so steps 4 j .. 4 j + 3 cover chunk rows 16 j .. 16 j + 15.
 __device__ inline int kidx128(int kk, int q) { return 32 * (kk >> 3) + 8 * q + (kk & 7); }
 __device__ inline int kidx64(int kk, int q) { return 16 * (kk >> 2) + 4 * q + (kk & 3); }
 
+// One wave's operands of one chunk, loaded a chunk ahead: each group is
+// loaded right after its last use in the chunk before.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const Params p) {
+struct Ops {
+  u32x4 ka[4], qa[4];     // k, q row 16 rb + l16 (the A operands of K S and Q S)
+  f32x4 va, vb, vq, vs;   // the row factors of rows 16 rb + 4 q4 .. + 3
+  float vv[4];            // v of those rows, this wave's column
+  f32x4 ta[4], aa[4];     // T, A row 16 rb + l16
+  uint32_t kt[16];        // k[kidx64(kk, q4)][32 rb + 2 l16 .. + 1]: the A operands of K^T D
+  float glast;
+};
+
+// Work group: one (run, value head, 32 state columns). Wave w computes the
+// 16 x 16 tile (rows 16 rb, columns 16 nb of the slice; nb = w / 4, rb = w % 4
+// or 3 - w % 4)
+// of Y, D and O, and state rows 32 rb .. 32 rb + 31 of those columns. Per
+// chunk, with jmax = (L - 1) / 16 the last row block holding run tokens:
+//   phase 0  K S and Q S together (one read of S), Y to LDS        barrier
+//   phase 1  D = T Y over row blocks j <= min(rb, jmax) (T is lower
+//            triangular, blocks past jmax are padding), D and Ds to LDS  barrier
+//   phase 2  O = (Q S) + A D (blocks j <= min(rb, jmax)), S <- gamma S + K^T Ds
+//            (blocks j <= jmax) into the other state buffer        barrier
+// A wave whose rows are all padding skips phases 0-1 and the O products.
+template <typename T>
+__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float smem[kLds];
   // work group b -> (unit u = r Hv + h, column block cb); the ncb groups of a
   // unit share b % 8 and so an XCD, whose L2 then serves their common reads
@@ -216,139 +273,149 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_kernel(const Params p) {
   const int u = (b / (8 * p.ncb)) * 8 + (b & 7), cb = (b >> 3) % p.ncb;
   if (u >= p.units) return;  // the whole group, before any barrier
   const int r = u / p.Hv, h = u % p.Hv, hk = h / (p.Hv / p.Hk);
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, q4 = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, q4 = lane >> 4;
+  // waves w and w + 4 share a SIMD: give them row blocks rb and 3 - rb, so
+  // every SIMD carries the same share of the triangular products
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nb = w >> 2, rb = nb ? 3 - (w & 3) : (w & 3);
   float *sY = smem + 2 * kDk * kSS, *sD = sY + kC * kSB, *sDs = sD + kC * kSB;
-  const int col0 = kCols * cb;
+  const int col0 = kCols * cb, col = 16 * nb + l16;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
-  for (int x = tid; x < kDk * kCols; x += kThreads)
+  for (int x = tid; x < kDk * kCols; x += kScanThreads)
     smem[(x / kCols) * kSS + x % kCols] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
   const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
   const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
   const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
-  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + col0;
-  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + col0;
-  const int ri = 16 * w + l16;  // the A-operand row of the 64-row products
+  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + col0 + col;
+  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + col0 + col;
+  const int ri = 16 * rb + l16;   // the A-operand row of the 64-row products
+  const int ro = 16 * rb + 4 * q4;  // the first of the lane's accumulator rows
+
+  // Loads of chunk (t0, slot s), rows clamped to the run (padding rows carry zero factors).
+  auto rec_of = [&](int s) __attribute__((always_inline)) { return p.rec + ((int64_t)s * p.Hv + h) * kRec; };
+  auto load0 = [&](Ops<T> &o, int t0, int s) __attribute__((always_inline)) {
+    const int L = min(kC, end - t0);
+    const int64_t tr = t0 + min(ri, L - 1);
+    const float *vec = rec_of(s) + 2 * kC * kC;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.ka[j] = *(const DAN_GLOBAL u32x4 *)(kh + tr * p.k_st + 32 * j + 8 * q4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.qa[j] = *(const DAN_GLOBAL u32x4 *)(qh + tr * p.q_st + 32 * j + 8 * q4);
+    o.va = *(const DAN_GLOBAL f32x4 *)(vec + 0 * kC + ro);
+    o.vb = *(const DAN_GLOBAL f32x4 *)(vec + 1 * kC + ro);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) o.vv[rr] = (float)*(const DAN_GLOBAL T *)(vh + (int64_t)(t0 + min(ro + rr, L - 1)) * p.v_st);
+  };
+  auto load1 = [&](Ops<T> &o, int s) __attribute__((always_inline)) {
+    const float *rec = rec_of(s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.ta[j] = *(const DAN_GLOBAL f32x4 *)(rec + ri * kC + 16 * j + 4 * q4);
+    o.vs = *(const DAN_GLOBAL f32x4 *)(rec + 2 * kC * kC + 3 * kC + ro);
+  };
+  auto load2 = [&](Ops<T> &o, int t0, int s) __attribute__((always_inline)) {
+    const int L = min(kC, end - t0);
+    const float *rec = rec_of(s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.aa[j] = *(const DAN_GLOBAL f32x4 *)(rec + kC * kC + ri * kC + 16 * j + 4 * q4);
+    o.vq = *(const DAN_GLOBAL f32x4 *)(rec + 2 * kC * kC + 2 * kC + ro);
+    o.glast = *(const DAN_GLOBAL float *)(rec + 2 * kC * kC + 4 * kC);
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+      o.kt[kk] = *(const DAN_GLOBAL uint32_t *)(kh + (int64_t)(t0 + min(kidx64(kk, q4), L - 1)) * p.k_st + 32 * rb + 2 * l16);
+  };
+
+  Ops<T> op;
+  int s = r + row0 / kC;
+  if (row0 < end) {
+    load0(op, row0, s);
+    load1(op, s);
+    load2(op, row0, s);
+  }
   int cur = 0;
   __syncthreads();
-  for (int t0 = row0, s = r + row0 / kC; t0 < end; t0 += kC, ++s) {
-    const int L = min(kC, end - t0);
-    const float *rec = p.rec + ((int64_t)s * p.Hv + h) * kRec;
-    const float *Tm = rec, *Am = rec + kC * kC, *vec = rec + 2 * kC * kC;
+  for (int t0 = row0; t0 < end; t0 += kC, ++s) {
+    const int L = min(kC, end - t0), jmax = (L - 1) >> 4;
+    const bool rows = 16 * rb < L;  // the wave's tile holds run tokens
+    const int jtop = min(rb, jmax);
+    // the next chunk (this one again after the last: the loads stay in bounds)
+    const bool more = t0 + kC < end;
+    const int tn = more ? t0 + kC : t0, sn = more ? s + 1 : s;
     float *sS = smem + cur * kDk * kSS, *sN = smem + (cur ^ 1) * kDk * kSS;
 
-    // operands, rows clamped to the run (padding rows carry zero factors)
-    const int64_t tr = t0 + min(ri, L - 1);
-    u32x4 ka[4], qa[4];
+    // phase 0: K S and Q S; Y = diag(beta) V - diag(beta gamma r_k) K S
+    f32x4 x = {}, o1 = {};
+    if (rows) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ka[j] = *(const DAN_GLOBAL u32x4 *)(kh + tr * p.k_st + 32 * j + 8 * q4);
-    const f32x4 va = *(const DAN_GLOBAL f32x4 *)(vec + 0 * kC + 16 * w + 4 * q4);
-    const f32x4 vb = *(const DAN_GLOBAL f32x4 *)(vec + 1 * kC + 16 * w + 4 * q4);
-    float vv[2][4];
+      for (int kk = 0; kk < 32; ++kk) {
+        const float bs = sS[kidx128(kk, q4) * kSS + col];
+        x = mma(half_of<T>(op.ka[kk >> 3][(kk & 7) >> 1], kk & 1), bs, x);
+        o1 = mma(half_of<T>(op.qa[kk >> 3][(kk & 7) >> 1], kk & 1), bs, o1);
+      }
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int64_t t = t0 + min(16 * w + 4 * q4 + rr, L - 1);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) vv[nb][rr] = (float)*(const DAN_GLOBAL T *)(vh + t * p.v_st + 16 * nb + l16);
+      for (int rr = 0; rr < 4; ++rr) sY[(ro + rr) * kSB + col] = op.vb[rr] * op.vv[rr] - op.va[rr] * x[rr];
     }
-    f32x4 ta[4], aa[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ta[j] = *(const DAN_GLOBAL f32x4 *)(Tm + ri * kC + 16 * j + 4 * q4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) qa[j] = *(const DAN_GLOBAL u32x4 *)(qh + tr * p.q_st + 32 * j + 8 * q4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) aa[j] = *(const DAN_GLOBAL f32x4 *)(Am + ri * kC + 16 * j + 4 * q4);
-    const f32x4 vq = *(const DAN_GLOBAL f32x4 *)(vec + 2 * kC + 16 * w + 4 * q4);
-    const f32x4 vs = *(const DAN_GLOBAL f32x4 *)(vec + 3 * kC + 16 * w + 4 * q4);
-    const float glast = *(const DAN_GLOBAL float *)(vec + 4 * kC);
-    uint32_t kt[16];  // k[i][32 w + 2 l16 .. + 1] for i = kidx64(kk, q4)
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk)
-      kt[kk] = *(const DAN_GLOBAL uint32_t *)(kh + (int64_t)(t0 + min(kidx64(kk, q4), L - 1)) * p.k_st + 32 * w + 2 * l16);
+    load0(op, tn, sn);
+    barrier_lds();
 
-    // Y = diag(beta) V - diag(beta gamma r_k) K S, rows 16 w .. 16 w + 15
-    f32x4 x[2] = {};
+    // phase 1: D = T Y
+    if (rows) {
+      f32x4 d = {};
 #pragma unroll
-    for (int kk = 0; kk < 32; ++kk) {
-      const float a = half_of<T>(ka[kk >> 3][(kk & 7) >> 1], kk & 1);
+      for (int j = 0; j < 4; ++j)  // static indices keep op in registers; the guard is wave-uniform
+        if (j <= jtop) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) x[nb] = mma(a, sS[kidx128(kk, q4) * kSS + 16 * nb + l16], x[nb]);
-    }
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sY[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = vb[rr] * vv[nb][rr] - va[rr] * x[nb][rr];
-    __syncthreads();
-
-    // D = T Y
-    f32x4 d[2] = {};
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      const float a = ta[kk >> 2][kk & 3];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) d[nb] = mma(a, sY[kidx64(kk, q4) * kSB + 16 * nb + l16], d[nb]);
-    }
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+          for (int e = 0; e < 4; ++e) d = mma(op.ta[j][e], sY[(16 * j + 4 * q4 + e) * kSB + col], d);
+        }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        sD[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = d[nb][rr];
-        sDs[(16 * w + 4 * q4 + rr) * kSB + 16 * nb + l16] = vs[rr] * d[nb][rr];
+        sD[(ro + rr) * kSB + col] = d[rr];
+        sDs[(ro + rr) * kSB + col] = op.vs[rr] * d[rr];
       }
-    __syncthreads();
+    }
+    load1(op, sn);
+    barrier_lds();
 
-    // O = diag(r_q Dk^-1/2 gamma) Q S + A D
-    f32x4 o1[2] = {}, o2[2] = {};
+    // phase 2: O = diag(r_q Dk^-1/2 gamma) Q S + A D; S <- gamma_63 S + K^T Ds
+    if (rows) {
+      f32x4 o2 = {};
 #pragma unroll
-    for (int kk = 0; kk < 32; ++kk) {
-      const float a = half_of<T>(qa[kk >> 3][(kk & 7) >> 1], kk & 1);
+      for (int j = 0; j < 4; ++j)
+        if (j <= jtop) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) o1[nb] = mma(a, sS[kidx128(kk, q4) * kSS + 16 * nb + l16], o1[nb]);
+          for (int e = 0; e < 4; ++e) o2 = mma(op.aa[j][e], sD[(16 * j + 4 * q4 + e) * kSB + col], o2);
+        }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (ro + rr < L) *(DAN_GLOBAL T *)(oh + (int64_t)(t0 + ro + rr) * p.o_st) = (T)(op.vq[rr] * o1[rr] + o2[rr]);
     }
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      const float a = aa[kk >> 2][kk & 3];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) o2[nb] = mma(a, sD[kidx64(kk, q4) * kSB + 16 * nb + l16], o2[nb]);
-    }
+    // the wave's state rows are 32 rb + 2 m + mb for row m of block mb (one
+    // 4-byte load of k gives both blocks' A operands)
+    f32x4 sn0, sn1;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const int i = 16 * w + 4 * q4 + rr;
-      if (i < L) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          *(DAN_GLOBAL T *)(oh + (int64_t)(t0 + i) * p.o_st + 16 * nb + l16) = (T)(vq[rr] * o1[nb][rr] + o2[nb][rr]);
-      }
+      sn0[rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col];
+      sn1[rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col];
     }
-
-    // S <- gamma_63 S + K^T diag(exp(G_63 - G) r_k) D; the wave's state rows
-    // are 32 w + 2 m + mb for row m of block mb (so one 4-byte load of k
-    // gives both blocks' A operands)
-    f32x4 sn[2][2];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int j = 0; j < 4; ++j)
+      if (j <= jmax) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sn[mb][nb][rr] = glast * sS[(32 * w + 2 * (4 * q4 + rr) + mb) * kSS + 16 * nb + l16];
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk)
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const float a = half_of<T>(kt[kk], mb);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) sn[mb][nb] = mma(a, sDs[kidx64(kk, q4) * kSB + 16 * nb + l16], sn[mb][nb]);
+        for (int e = 0; e < 4; ++e) {
+          const float bd = sDs[(16 * j + 4 * q4 + e) * kSB + col];
+          sn0 = mma(half_of<T>(op.kt[4 * j + e], 0), bd, sn0);
+          sn1 = mma(half_of<T>(op.kt[4 * j + e], 1), bd, sn1);
+        }
       }
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sN[(32 * w + 2 * (4 * q4 + rr) + mb) * kSS + 16 * nb + l16] = sn[mb][nb][rr];
-    __syncthreads();  // the new state is whole, and every read of this chunk's Y, D and S is done
+    for (int rr = 0; rr < 4; ++rr) {
+      sN[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col] = sn0[rr];
+      sN[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col] = sn1[rr];
+    }
+    load2(op, tn, sn);
+    barrier_lds();  // the new state is whole, and every read of this chunk's Y, D and S is done
     cur ^= 1;
   }
   const float *sS = smem + cur * kDk * kSS;
-  for (int x = tid; x < kDk * kCols; x += kThreads)
+  for (int x = tid; x < kDk * kCols; x += kScanThreads)
     *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols) = sS[(x / kCols) * kSS + x % kCols];
 }
 
@@ -361,28 +428,26 @@ int64_t dan_gdn_chunk_record_bytes(int32_t num_tokens, int32_t num_runs, int32_t
   return dan_gdnc::slots(num_tokens, num_runs) * num_v_heads * dan_gdnc::kRec * 4;
 }
 
-// The chunked form; arguments already checked by dan_gdn_fwd, `norms` the
-// workspace's norm factors and `records` its 16-byte aligned chunk records.
-hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *norms, float *records, hipStream_t s) {
+// The chunked form; arguments already checked by dan_gdn_fwd, `records` the
+// workspace (16-byte aligned).
+hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t s) {
   dan_gdnc::Params p;
   p.cu = a->cu; p.q = a->q; p.k = a->k; p.v = a->v;
   p.q_st = a->q_stride_tok; p.q_sh = a->q_stride_head; p.k_st = a->k_stride_tok; p.k_sh = a->k_stride_head;
   p.v_st = a->v_stride_tok; p.v_sh = a->v_stride_head; p.o_st = a->o_stride_tok; p.o_sh = a->o_stride_head;
   p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
-  p.norms = norms; p.rec = records;
+  p.rec = records;
   p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
   p.ncb = a->v_dim / dan_gdnc::kCols; p.units = a->num_runs * a->num_v_heads;
   const int64_t prep = dan_gdnc::slots(a->num_tokens, a->num_runs) * a->num_v_heads;
   const int64_t scan = ((int64_t)p.units + 7) / 8 * 8 * p.ncb;
-  hipError_t err = dan_gdn::launch_norms(a, norms, s);
-  if (err != hipSuccess) return err;
   const dim3 block(dan_gdnc::kThreads);
   if (a->dtype == DAN_DTYPE_BF16) {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<__bf16>, dim3((unsigned)prep), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<__bf16>, dim3((unsigned)scan), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<__bf16>, dim3((unsigned)scan), dim3(dan_gdnc::kScanThreads), 0, s, p);
   } else {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<_Float16>, dim3((unsigned)prep), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<_Float16>, dim3((unsigned)scan), block, 0, s, p);
+    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<_Float16>, dim3((unsigned)scan), dim3(dan_gdnc::kScanThreads), 0, s, p);
   }
   return hipGetLastError();
 }

@@ -62,8 +62,8 @@ typedef struct {
   float *states_out;      /* [R, Hv, Dk, Dv] (may equal states_in) */
   void *out; int64_t o_stride_tok, o_stride_head; /* [N, Hv, Dv] */
   /* Device scratch of at least dan_gdn_workspace_size(form, N, R, Hk, Hv, Dv)
-   * bytes, 16-byte aligned: the per-token l2-norm factors of q and k, and
-   * for the chunked form each chunk's triangular factors. */
+   * bytes, 16-byte aligned: the token form's per-token l2-norm factors of q
+   * and k, or the chunked form's per-chunk factors. */
   void *workspace; int64_t workspace_bytes;
   int32_t form;     /* DanGdnForm */
   int32_t reserved; /* 0 */
@@ -75,7 +75,8 @@ typedef struct {
 int dan_gdn_fwd(const DanGdnArgs *args, void *stream);
 
 /* Workspace bytes for dan_gdn_fwd; 0 for arguments it would reject. The
- * chunked form's part grows as (R + N / 64) Hv 34 KiB. */
+ * token form's grows as 8 N Hk bytes, the chunked form's as
+ * (R + N / 64) Hv 34 KiB. */
 int64_t dan_gdn_workspace_size(int32_t form, int32_t num_tokens, int32_t num_runs, int32_t num_k_heads,
                                int32_t num_v_heads, int32_t v_dim);
 
