@@ -398,8 +398,8 @@ def bench_gdn(args):
         "dtype": "fp32 state, bf16 io", "data": "synthetic",
         "config": {"workload": f"gdn-c3: {len(trunks)} trunks (longest {max(tl)}), {len(bl)} branches, {tokens} tokens, "
                                f"{hk}/{hv} heads, Dk = Dv = {d}", "seed": args.seed},
-        "roofline": {"bound": "fp32 MFMA, sequential in chunks of 64 tokens per run (trunks in the chunked form; "
-                              "branches shorter than deltanet.CHUNK_MIN_RUN token by token on the VALU)",
+        "roofline": {"bound": "fp32 MFMA, sequential in chunks of 64 tokens per run (the chunked form; a phase "
+                              "whose longest run is under deltanet.CHUNK_MIN_RUN tokens goes token by token)",
                      "achieved": round(flops / wall / 1e12, 2),
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
                      "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4), "forms": forms,
@@ -407,6 +407,39 @@ def bench_gdn(args):
         "layer": layer,
         "cpu_baseline": cpu,
     }), flush=True)
+
+
+def bench_gdn_forms(args):
+    """Both delta rule forms on synthetic phases of R runs of L tokens (16/16
+    heads, Dk = Dv = 128, bf16): the measurement behind deltanet.CHUNK_MIN_RUN.
+    Prints one JSON line per (R, L) with each form's median ms per call."""
+    from dan_amd.deltanet import delta_rule
+
+    dev = torch.device("cuda:0")
+    for r in (45, 200):
+        for ln in (4, 8, 16, 24, 32, 48, 64, 96, 128, 256):
+            n = r * ln
+            g = torch.Generator(device=dev).manual_seed(args.seed)
+            q = torch.randn(n, 16, 128, device=dev, generator=g).bfloat16()
+            k = torch.randn(n, 16, 128, device=dev, generator=g).bfloat16()
+            v = torch.randn(n, 16, 128, device=dev, generator=g).bfloat16()
+            gate = -(torch.rand(n, 16, device=dev, generator=g) * 0.1)
+            beta = torch.rand(n, 16, device=dev, generator=g)
+            st = torch.randn(r, 16, 128, 128, device=dev, generator=g) * 0.05
+            ms = {}
+            for form in ("token", "chunk"):
+                fn = lambda: delta_rule(q, k, v, gate, beta, [ln] * r, st, form=form)
+                for _ in range(3):
+                    fn()
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+                for e0, e1 in ev:
+                    e0.record()
+                    fn()
+                    e1.record()
+                torch.cuda.synchronize()
+                ms[form] = round(statistics.median(e0.elapsed_time(e1) for e0, e1 in ev), 4)
+            print(json.dumps({"runs": r, "run_tokens": ln, "token_ms": ms["token"], "chunk_ms": ms["chunk"]}),
+                  flush=True)
 
 
 def _gdn_layer_times(args, w, hk, hv, d, dev, hidden=2048, kernel=4):
@@ -524,6 +557,8 @@ def main():
                     help="measure one Llama-3-8B decoder layer's FP8 linears (quantize + hipBLASLt GEMM) at 8192 tokens")
     ap.add_argument("--gdn", action="store_true",
                     help="measure the Gated DeltaNet recurrence of one layer over the c3 tree batch")
+    ap.add_argument("--gdn-forms", action="store_true",
+                    help="time both delta rule forms on phases of R runs of L tokens (the form threshold)")
     ap.add_argument("--plan", action="store_true",
                     help="measure per-forward tile planning (host planner against the device planner) on --workload")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -549,6 +584,9 @@ def main():
         return
     if args.gdn:
         bench_gdn(args)
+        return
+    if args.gdn_forms:
+        bench_gdn_forms(args)
         return
     if args.front:
         if args.workload not in FRONT_SHAPES:

@@ -224,7 +224,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
 // columns: rows 8 apart in S, 4 apart in the others) hits 64 distinct banks.
 constexpr int kSS = 34, kSB = 36;
 constexpr int kLds = 2 * kDk * kSS + 3 * kC * kSB;
-constexpr int kScanThreads = 512;  // 8 waves: 4 row blocks x 2 column halves of the slice
+// The scan runs as 8 waves (one 16 x 16 tile each; for long runs, where a
+// chunk step's latency sets the pace) or as 4 waves (16 x 32 each; two work
+// groups per CU, for phases of many short runs, where the per-group fixed
+// cost does).
+constexpr int kScanLongWaves = 8, kScanShortWaves = 4;
 
 __device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
@@ -242,30 +246,34 @@ __device__ inline int kidx128(int kk, int q) { return 32 * (kk >> 3) + 8 * q + (
 __device__ inline int kidx64(int kk, int q) { return 16 * (kk >> 2) + 4 * q + (kk & 3); }
 
 // One wave's operands of one chunk, loaded a chunk ahead: each group is
-// loaded right after its last use in the chunk before.
-template <typename T>
+// loaded right after its last use in the chunk before. NC: the wave's
+// 16-column halves of the slice.
+template <typename T, int NC>
 struct Ops {
   u32x4 ka[4], qa[4];     // k, q row 16 rb + l16 (the A operands of K S and Q S)
   f32x4 va, vb, vq, vs;   // the row factors of rows 16 rb + 4 q4 .. + 3
-  float vv[4];            // v of those rows, this wave's column
+  float vv[NC][4];        // v of those rows, the wave's columns
   f32x4 ta[4], aa[4];     // T, A row 16 rb + l16
   uint32_t kt[16];        // k[kidx64(kk, q4)][32 rb + 2 l16 .. + 1]: the A operands of K^T D
   float glast;
 };
 
-// Work group: one (run, value head, 32 state columns). Wave w computes the
-// 16 x 16 tile (rows 16 rb, columns 16 nb of the slice; nb = w / 4, rb = w % 4
-// or 3 - w % 4)
-// of Y, D and O, and state rows 32 rb .. 32 rb + 31 of those columns. Per
-// chunk, with jmax = (L - 1) / 16 the last row block holding run tokens:
+// Work group: one (run, value head, 32 state columns). Wave w computes rows
+// 16 rb .. 16 rb + 15 of Y, D and O in its NC column halves, and state rows
+// 32 rb .. 32 rb + 31 of those columns: with 8 waves, half nb = w / 4 and
+// rb = w % 4 or 3 - w % 4 (waves w and w + 4 share a SIMD, so every SIMD
+// carries the same share of the triangular products); with 4 waves, rb = w
+// and both halves. Per chunk, with jmax = (L - 1) / 16 the last row block
+// holding run tokens:
 //   phase 0  K S and Q S together (one read of S), Y to LDS        barrier
 //   phase 1  D = T Y over row blocks j <= min(rb, jmax) (T is lower
 //            triangular, blocks past jmax are padding), D and Ds to LDS  barrier
 //   phase 2  O = (Q S) + A D (blocks j <= min(rb, jmax)), S <- gamma S + K^T Ds
 //            (blocks j <= jmax) into the other state buffer        barrier
 // A wave whose rows are all padding skips phases 0-1 and the O products.
-template <typename T>
-__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p) {
+template <typename T, int W>
+__global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
+  constexpr int NC = 8 / W;
   __shared__ __attribute__((aligned(16))) float smem[kLds];
   // work group b -> (unit u = r Hv + h, column block cb); the ncb groups of a
   // unit share b % 8 and so an XCD, whose L2 then serves their common reads
@@ -274,25 +282,27 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p
   if (u >= p.units) return;  // the whole group, before any barrier
   const int r = u / p.Hv, h = u % p.Hv, hk = h / (p.Hv / p.Hk);
   const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, q4 = lane >> 4;
-  // waves w and w + 4 share a SIMD: give them row blocks rb and 3 - rb, so
-  // every SIMD carries the same share of the triangular products
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nb = w >> 2, rb = nb ? 3 - (w & 3) : (w & 3);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb0 = W == 8 ? w >> 2 : 0, rb = W == 8 ? (nb0 ? 3 - (w & 3) : (w & 3)) : w;
   float *sY = smem + 2 * kDk * kSS, *sD = sY + kC * kSB, *sDs = sD + kC * kSB;
-  const int col0 = kCols * cb, col = 16 * nb + l16;
+  const int col0 = kCols * cb;
+  int col[NC];
+#pragma unroll
+  for (int n = 0; n < NC; ++n) col[n] = 16 * (nb0 + n) + l16;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
-  for (int x = tid; x < kDk * kCols; x += kScanThreads)
+  for (int x = tid; x < kDk * kCols; x += 64 * W)
     smem[(x / kCols) * kSS + x % kCols] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
   const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
   const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
   const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
-  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + col0 + col;
-  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + col0 + col;
+  const T *vh = static_cast<const T *>(p.v) + (int64_t)h * p.v_sh + col0;
+  T *oh = static_cast<T *>(p.o) + (int64_t)h * p.o_sh + col0;
   const int ri = 16 * rb + l16;   // the A-operand row of the 64-row products
   const int ro = 16 * rb + 4 * q4;  // the first of the lane's accumulator rows
 
   // Loads of chunk (t0, slot s), rows clamped to the run (padding rows carry zero factors).
   auto rec_of = [&](int s) __attribute__((always_inline)) { return p.rec + ((int64_t)s * p.Hv + h) * kRec; };
-  auto load0 = [&](Ops<T> &o, int t0, int s) __attribute__((always_inline)) {
+  auto load0 = [&](Ops<T, NC> &o, int t0, int s) __attribute__((always_inline)) {
     const int L = min(kC, end - t0);
     const int64_t tr = t0 + min(ri, L - 1);
     const float *vec = rec_of(s) + 2 * kC * kC;
@@ -303,15 +313,18 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p
     o.va = *(const DAN_GLOBAL f32x4 *)(vec + 0 * kC + ro);
     o.vb = *(const DAN_GLOBAL f32x4 *)(vec + 1 * kC + ro);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) o.vv[rr] = (float)*(const DAN_GLOBAL T *)(vh + (int64_t)(t0 + min(ro + rr, L - 1)) * p.v_st);
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        o.vv[n][rr] = (float)*(const DAN_GLOBAL T *)(vh + (int64_t)(t0 + min(ro + rr, L - 1)) * p.v_st + col[n]);
   };
-  auto load1 = [&](Ops<T> &o, int s) __attribute__((always_inline)) {
+  auto load1 = [&](Ops<T, NC> &o, int s) __attribute__((always_inline)) {
     const float *rec = rec_of(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.ta[j] = *(const DAN_GLOBAL f32x4 *)(rec + ri * kC + 16 * j + 4 * q4);
     o.vs = *(const DAN_GLOBAL f32x4 *)(rec + 2 * kC * kC + 3 * kC + ro);
   };
-  auto load2 = [&](Ops<T> &o, int t0, int s) __attribute__((always_inline)) {
+  auto load2 = [&](Ops<T, NC> &o, int t0, int s) __attribute__((always_inline)) {
     const int L = min(kC, end - t0);
     const float *rec = rec_of(s);
 #pragma unroll
@@ -323,7 +336,7 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p
       o.kt[kk] = *(const DAN_GLOBAL uint32_t *)(kh + (int64_t)(t0 + min(kidx64(kk, q4), L - 1)) * p.k_st + 32 * rb + 2 * l16);
   };
 
-  Ops<T> op;
+  Ops<T, NC> op;
   int s = r + row0 / kC;
   if (row0 < end) {
     load0(op, row0, s);
@@ -342,80 +355,111 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const Params p
     float *sS = smem + cur * kDk * kSS, *sN = smem + (cur ^ 1) * kDk * kSS;
 
     // phase 0: K S and Q S; Y = diag(beta) V - diag(beta gamma r_k) K S
-    f32x4 x = {}, o1 = {};
+    f32x4 x[NC], o1[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) x[n] = o1[n] = f32x4{};
     if (rows) {
 #pragma unroll
       for (int kk = 0; kk < 32; ++kk) {
-        const float bs = sS[kidx128(kk, q4) * kSS + col];
-        x = mma(half_of<T>(op.ka[kk >> 3][(kk & 7) >> 1], kk & 1), bs, x);
-        o1 = mma(half_of<T>(op.qa[kk >> 3][(kk & 7) >> 1], kk & 1), bs, o1);
+        const float ak = half_of<T>(op.ka[kk >> 3][(kk & 7) >> 1], kk & 1);
+        const float aq = half_of<T>(op.qa[kk >> 3][(kk & 7) >> 1], kk & 1);
+#pragma unroll
+        for (int n = 0; n < NC; ++n) {
+          const float bs = sS[kidx128(kk, q4) * kSS + col[n]];
+          x[n] = mma(ak, bs, x[n]);
+          o1[n] = mma(aq, bs, o1[n]);
+        }
       }
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sY[(ro + rr) * kSB + col] = op.vb[rr] * op.vv[rr] - op.va[rr] * x[rr];
+      for (int n = 0; n < NC; ++n)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sY[(ro + rr) * kSB + col[n]] = op.vb[rr] * op.vv[n][rr] - op.va[rr] * x[n][rr];
     }
     load0(op, tn, sn);
     barrier_lds();
 
     // phase 1: D = T Y
     if (rows) {
-      f32x4 d = {};
+      f32x4 d[NC];
+#pragma unroll
+      for (int n = 0; n < NC; ++n) d[n] = f32x4{};
 #pragma unroll
       for (int j = 0; j < 4; ++j)  // static indices keep op in registers; the guard is wave-uniform
         if (j <= jtop) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) d = mma(op.ta[j][e], sY[(16 * j + 4 * q4 + e) * kSB + col], d);
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int n = 0; n < NC; ++n) d[n] = mma(op.ta[j][e], sY[(16 * j + 4 * q4 + e) * kSB + col[n]], d[n]);
         }
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        sD[(ro + rr) * kSB + col] = d[rr];
-        sDs[(ro + rr) * kSB + col] = op.vs[rr] * d[rr];
-      }
+      for (int n = 0; n < NC; ++n)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          sD[(ro + rr) * kSB + col[n]] = d[n][rr];
+          sDs[(ro + rr) * kSB + col[n]] = op.vs[rr] * d[n][rr];
+        }
     }
     load1(op, sn);
     barrier_lds();
 
     // phase 2: O = diag(r_q Dk^-1/2 gamma) Q S + A D; S <- gamma_63 S + K^T Ds
     if (rows) {
-      f32x4 o2 = {};
+      f32x4 o2[NC];
+#pragma unroll
+      for (int n = 0; n < NC; ++n) o2[n] = f32x4{};
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (j <= jtop) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o2 = mma(op.aa[j][e], sD[(16 * j + 4 * q4 + e) * kSB + col], o2);
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int n = 0; n < NC; ++n) o2[n] = mma(op.aa[j][e], sD[(16 * j + 4 * q4 + e) * kSB + col[n]], o2[n]);
         }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        if (ro + rr < L) *(DAN_GLOBAL T *)(oh + (int64_t)(t0 + ro + rr) * p.o_st) = (T)(op.vq[rr] * o1[rr] + o2[rr]);
+        if (ro + rr < L) {
+#pragma unroll
+          for (int n = 0; n < NC; ++n)
+            *(DAN_GLOBAL T *)(oh + (int64_t)(t0 + ro + rr) * p.o_st + col[n]) = (T)(op.vq[rr] * o1[n][rr] + o2[n][rr]);
+        }
     }
     // the wave's state rows are 32 rb + 2 m + mb for row m of block mb (one
     // 4-byte load of k gives both blocks' A operands)
-    f32x4 sn0, sn1;
+    f32x4 sn0[NC], sn1[NC];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      sn0[rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col];
-      sn1[rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col];
-    }
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        sn0[n][rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col[n]];
+        sn1[n][rr] = op.glast * sS[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col[n]];
+      }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (j <= jmax) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float bd = sDs[(16 * j + 4 * q4 + e) * kSB + col];
-          sn0 = mma(half_of<T>(op.kt[4 * j + e], 0), bd, sn0);
-          sn1 = mma(half_of<T>(op.kt[4 * j + e], 1), bd, sn1);
+          const float a0 = half_of<T>(op.kt[4 * j + e], 0), a1 = half_of<T>(op.kt[4 * j + e], 1);
+#pragma unroll
+          for (int n = 0; n < NC; ++n) {
+            const float bd = sDs[(16 * j + 4 * q4 + e) * kSB + col[n]];
+            sn0[n] = mma(a0, bd, sn0[n]);
+            sn1[n] = mma(a1, bd, sn1[n]);
+          }
         }
       }
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      sN[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col] = sn0[rr];
-      sN[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col] = sn1[rr];
-    }
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        sN[(32 * rb + 2 * (4 * q4 + rr)) * kSS + col[n]] = sn0[n][rr];
+        sN[(32 * rb + 2 * (4 * q4 + rr) + 1) * kSS + col[n]] = sn1[n][rr];
+      }
     load2(op, tn, sn);
     barrier_lds();  // the new state is whole, and every read of this chunk's Y, D and S is done
     cur ^= 1;
   }
   const float *sS = smem + cur * kDk * kSS;
-  for (int x = tid; x < kDk * kCols; x += kScanThreads)
+  for (int x = tid; x < kDk * kCols; x += 64 * W)
     *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols) = sS[(x / kCols) * kSS + x % kCols];
 }
 
@@ -441,13 +485,19 @@ hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t 
   p.ncb = a->v_dim / dan_gdnc::kCols; p.units = a->num_runs * a->num_v_heads;
   const int64_t prep = dan_gdnc::slots(a->num_tokens, a->num_runs) * a->num_v_heads;
   const int64_t scan = ((int64_t)p.units + 7) / 8 * 8 * p.ncb;
+  // Runs of DAN_GDN_SHORT_RUN tokens or fewer on average: the 4-wave scan
+  // (two work groups per CU); longer: the 8-wave scan (shorter chunk steps).
+  const bool shortrun = (int64_t)a->num_tokens <= (int64_t)DAN_GDN_SHORT_RUN * a->num_runs;
   const dim3 block(dan_gdnc::kThreads);
+  const dim3 sblock(64 * (shortrun ? dan_gdnc::kScanShortWaves : dan_gdnc::kScanLongWaves));
   if (a->dtype == DAN_DTYPE_BF16) {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<__bf16>, dim3((unsigned)prep), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<__bf16>, dim3((unsigned)scan), dim3(dan_gdnc::kScanThreads), 0, s, p);
+    if (shortrun) hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<__bf16, dan_gdnc::kScanShortWaves>), dim3((unsigned)scan), sblock, 0, s, p);
+    else hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<__bf16, dan_gdnc::kScanLongWaves>), dim3((unsigned)scan), sblock, 0, s, p);
   } else {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<_Float16>, dim3((unsigned)prep), block, 0, s, p);
-    hipLaunchKernelGGL(dan_gdnc::chunk_scan_kernel<_Float16>, dim3((unsigned)scan), dim3(dan_gdnc::kScanThreads), 0, s, p);
+    if (shortrun) hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<_Float16, dan_gdnc::kScanShortWaves>), dim3((unsigned)scan), sblock, 0, s, p);
+    else hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<_Float16, dan_gdnc::kScanLongWaves>), dim3((unsigned)scan), sblock, 0, s, p);
   }
   return hipGetLastError();
 }

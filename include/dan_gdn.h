@@ -33,6 +33,10 @@ extern "C" {
 
 /* Tokens per chunk of the chunked form. */
 #define DAN_GDN_CHUNK 64
+/* The chunked form walks calls whose runs average at most this many tokens
+ * with a scan tuned for many short runs, other calls with one tuned for the
+ * latency of long runs (same results). */
+#define DAN_GDN_SHORT_RUN 256
 
 /* How dan_gdn_fwd walks a run. Both give the same recurrence within fp32
  * rounding: the token form steps token by token (a run's results do not
