@@ -349,6 +349,11 @@ def bench_gdn(args):
         ob, _ = delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, ft.index_select(0, bseg))
         out[brow] = ob
 
+    t_settle = time.perf_counter()  # the clock settles under sustained steps (see --settle-ms)
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
