@@ -1146,11 +1146,16 @@ void tree_attn_kernel(const KParams args) {
 #pragma unroll
       for (int jp = 0; jp < 2; ++jp) {
         const Out4<TOut> e = pack_out<TOut>(o[db], 8 * jp, linv), od = pack_out<TOut>(o[db], 8 * jp + 4, linv);
-        const Out4<TOut> give = hl ? e : od, keep = hl ? od : e;
-        Out4<TOut> got;
+        // v_permlane32_swap(e, od) leaves lanes below 32 (e, partner's e) and lanes from 32
+        // (partner's od, od): each lane's 8 contiguous d in order, with no select.
+        Out4<TOut> first, second;
 #pragma unroll
-        for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) got.w[w4] = __shfl_xor(give.w[w4], 32);
-        if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), hl ? got : keep, hl ? keep : got);
+        for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(e.w[w4], od.w[w4], false, false);
+          first.w[w4] = sw[0];
+          second.w[w4] = sw[1];
+        }
+        if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), first, second);
       }
     gbase += ntile;
     pre = nn;
