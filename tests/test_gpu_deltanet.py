@@ -100,6 +100,23 @@ def test_chunk_scan_variants_bit_identical(gpu):
     assert torch.equal(o8, o4) and torch.equal(f8, f4[:2])
 
 
+@pytest.mark.parametrize("form", ["token", "chunk"])
+def test_repeated_keys(gpu, form):
+    """Every key one of two vectors, beta = 1 and no decay: I + L is as far
+    from the identity as it gets (its off-diagonal entries are +-1 and 1), and
+    the chunked form's triangular inverse must still follow the recurrence."""
+    say(f"delta rule {form}: repeated keys, beta 1, no decay")
+    lengths = [200, 70]
+    q, k, v, g, b, st = inputs(lengths, 1, 2, 128, torch.bfloat16, gpu, seed=9)
+    k = k[:2].repeat((sum(lengths) + 1) // 2, 1, 1)[:sum(lengths)].contiguous()
+    g = torch.zeros_like(g)
+    b = torch.ones_like(b)
+    out, fin = delta_rule(q, k, v, g, b, lengths, st, form=form)
+    torch.cuda.synchronize()
+    ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), lengths, st.cpu(), recurrent=True)
+    check(out, fin, ref_o, ref_f, torch.bfloat16)
+
+
 def test_chunk_form_split_run(gpu):
     say("delta rule, chunked form: one run of 400 tokens vs two calls (150 + 250)")
     q, k, v, g, b, st = inputs([400], 2, 2, 128, torch.bfloat16, gpu, seed=1)
