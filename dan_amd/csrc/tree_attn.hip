@@ -33,19 +33,20 @@
 //                                softmax state; row max/sum need one cross-half
 //                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max is not recomputed per tile, only raised when a tile's row sum shows
-//   that P left fp16's range (kSumLimit), so the O accumulators are rarely
-//   rescaled.
+//   max is not recomputed per tile, only raised when a tile's largest score
+//   would put p above 2^kLog2Limit (fp16's range), so the O accumulators are
+//   rarely rescaled.
 //   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
 //                                B = P^T straight from the S^T registers: K rows
 //                                are staged in a permuted order that makes the
 //                                S^T accumulator layout the B-operand layout.
 // Staging: K and V^T tiles go from global memory straight into LDS
-// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep, into
-// rows padded by 16 bytes (conflict-free operand reads at constant offsets).
+// (global_load_lds_dwordx4, no registers, no VALU), four buffers deep, each
+// K row's 16-byte chunks XOR-swizzled (conflict-free operand reads).
 // Pipelining: while the softmax of tile j runs on the VALU, the wave already
-// issues S = K Q^T of tile j+1 on the matrix core; the tile two ahead is in
-// flight from memory.
+// issues S = K Q^T of tile j+1 on the matrix core (into the same registers,
+// each as soon as the softmax has read it); the tile two ahead is in flight
+// from memory.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -82,7 +83,7 @@ inline int waves_for(int head_dim) { return head_dim == 256 ? Shape<256>::waves 
 // its S products alone meanwhile: the two waves of a SIMD settle half a phase
 // apart.
 constexpr int kIssuers = 4;
-constexpr float kSumLimit = 32768.0f;             // per-lane partial row sum of P: keeps p <= 2^15
+constexpr float kLog2Limit = 15.0f;  // p = exp2(S c - m) <= 2^15: P stays inside fp16's range
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -955,12 +956,12 @@ void tree_attn_kernel(const KParams args) {
     // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
     // partial row sum of the fp16-rounded values that P V uses (exact products,
     // fp32 accumulation), so rounding P mostly cancels in O / l. The running
-    // max m is not recomputed per tile: a partial row sum above kSumLimit (or
-    // inf) means some p left fp16's range or m is stale by more than
-    // log2(kSumLimit / 32); only then is m raised to the tile's max (O and l
-    // rescaled) and the tile's P redone. A lane holds half of its query's keys
-    // and the other half sits in lane ^ 32; both keep the same m.
-    auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
+    // max m is not recomputed per tile: before a tile's exponentials, a lane
+    // score above m + kLog2Limit (or a NaN) in any lane raises m to the tile's
+    // max (O and l rescaled), so every p stays below 2^15. The check reads S
+    // only, so P V does not wait on the row sum. A lane holds half of its
+    // query's keys and the other half sits in lane ^ 32; both keep the same m.
+    auto lane_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the lane's 32 keys
       float m8[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
@@ -968,7 +969,10 @@ void tree_attn_kernel(const KParams args) {
       for (int w2 = 4; w2 >= 1; w2 >>= 1)
 #pragma unroll
         for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
-      const LanePair mp = lane_pair(m8[0]);
+      return m8[0];
+    };
+    auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
+      const LanePair mp = lane_pair(lane_max(s));
       return fmaxf(mp.self, mp.other);
     };
     auto exp_phase = [&](const f32x16(&s)[2], float c) __attribute__((always_inline)) {
@@ -994,12 +998,12 @@ void tree_attn_kernel(const KParams args) {
       }
       return (acc[0] + acc[1]) + (acc[2] + acc[3]);
     };
-    // Accept the tile's P (partial sum ts), raising m to the tile's max (and
-    // redoing P) first if it overflowed; and bring O to the scale of the
-    // tile's V^T block (2^ve) if it differs from O's (2^vE). Both are rare
-    // and share one branch.
-    auto finish_tile = [&](const f32x16(&s)[2], float ts, float c, int ve) __attribute__((always_inline)) {
-      const bool raise = __any(!(ts <= kSumLimit));
+    // Before a tile's softmax: raise m to the tile's max if some score would
+    // put p above 2^kLog2Limit, and bring O to the scale of the tile's V^T
+    // block (2^ve) if it differs from O's (2^vE). Both are rare and share one
+    // branch.
+    auto begin_tile = [&](const f32x16(&s)[2], float c, int ve) __attribute__((always_inline)) {
+      const bool raise = __any(!(fmaf(lane_max(s), c, mneg) <= kLog2Limit));
       if (raise || ve != vE) {
         float f = exp2i(vE - ve);
         if (raise) {
@@ -1009,16 +1013,14 @@ void tree_attn_kernel(const KParams args) {
           mneg = -mnew;
           lsum *= alpha;
           f *= alpha;
-          ts = exp_phase(s, c);
         }
 #pragma unroll
         for (int db = 0; db < ND; ++db) o[db] *= f;
         vE = ve;
       }
-      lsum += ts;
     };
     // O^T += V^T P^T over the 64 keys of stage buffer b (its V^T block is at
-    // O's scale: finish_tile).
+    // O's scale: begin_tile).
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
       const uint8_t *vbuf = smem + b * L::buf + v_lane;
 #pragma unroll
@@ -1052,8 +1054,8 @@ void tree_attn_kernel(const KParams args) {
         fix_straddle(tile_of(it), s);
         const float c = tile_c(tile_of(it));
         if (it == 0) mneg = -fmaxf(s_max(s) * c, -3.0e38f);
-        const float ts = exp_phase(s, c);
-        finish_tile(s, ts, c, ve);
+        begin_tile(s, c, ve);
+        lsum += exp_phase(s, c);
         pv_phase((gbase + it) & (NB - 1));
       }
       nn = 0;
@@ -1074,34 +1076,36 @@ void tree_attn_kernel(const KParams args) {
       q_ready = false;
       wait_vmem<0>();
       barrier_lds();
-      f32x16 sa[2], sb[2];
+      f32x16 sc[2];  // S of the current tile
       // The running max m starts at the largest visible score of the first
       // tile (exact, so that tile's largest p is 1). A query that sees no key
       // of the first tile (only when the segment has neither past nor trunk)
       // starts from m = -3e38: its p stay 0 while its keys are hidden, and its
-      // first visible key overflows the tile's row sum, which raises m to that
-      // tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0). Finite
-      // throughout, so no inf - inf.
-      qk_phase(gbase & (NB - 1), sa);
-      mask_phase(tile_of(0), sa);
-      fix_straddle(tile_of(0), sa);
-      mneg = -fmaxf(s_max(sa) * tile_c(tile_of(0)), -3.0e38f);
+      // first visible key scores far above m + kLog2Limit, which raises m to
+      // that tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0).
+      // Finite throughout, so no inf - inf.
+      qk_phase(gbase & (NB - 1), sc);
+      mask_phase(tile_of(0), sc);
+      fix_straddle(tile_of(0), sc);
+      mneg = -fmaxf(s_max(sc) * tile_c(tile_of(0)), -3.0e38f);
 
       // Step `it`: P of tile it (VALU) while S of tile it+1 runs on the matrix
-      // core, then O += V P of tile it while the VALU masks S(it+1). The last
-      // step of the unit has no next tile. Every step starts with a barrier,
+      // core, then O += V P of tile it while the VALU masks S(it+1). S(it+1)
+      // goes to the registers of S(it): each product starts once the softmax
+      // has read the scores it overwrites. The last step of the unit has no
+      // next tile. Every step starts with a barrier,
       // after which tile it+3 of the concatenation (this unit, then the next
       // unit's first tiles) is issued into the buffer that tile it-1 used:
       // every wave has finished tile it-1 before the barrier.
       int it = 0;
-      auto step = [&](auto last, f32x16(&cur_s)[2], f32x16(&nxt_s)[2]) {
+      auto step = [&](auto last, f32x16(&s)[2]) {
         constexpr bool kLast = decltype(last)::value;
         if (!kLast && wave < kIssuers) {
           if (issued_cat(it + 2)) wait_vmem<SLOTS>();  // tile it+1 landed; it+2 may be in flight
           else wait_vmem<0>();
         }
         barrier_lds();
-        const int ve = load_scalar(vexp_u + tile_of(it));  // the tile's V^T exponent (finish_tile)
+        const int ve = load_scalar(vexp_u + tile_of(it));  // the tile's V^T exponent (begin_tile)
         // The issuing waves load tile it+3 now (see kIssuers).
         if (wave < kIssuers) issue_cat(it + 3);
         if (kLast && nn > 0) {  // q and key_lo of the next unit (this unit's are no longer used)
@@ -1109,29 +1113,21 @@ void tree_attn_kernel(const KParams args) {
           q_ready = true;
         }
         const float c = tile_c(tile_of(it));
-        const float ts = exp_phase(cur_s, c);
-        if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), nxt_s);
-        finish_tile(cur_s, ts, c, ve);
+        begin_tile(s, c, ve);
+        const float ts = exp_phase(s, c);
+        if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), s);
+        lsum += ts;
         pv_phase((gbase + it) & (NB - 1));
         if (!kLast) {
-          mask_phase(tile_of(it + 1), nxt_s);
-          fix_straddle(tile_of(it + 1), nxt_s);
+          mask_phase(tile_of(it + 1), s);
+          fix_straddle(tile_of(it + 1), s);
         }
         ++it;
       };
       using NotLast = std::integral_constant<bool, false>;
       using Last = std::integral_constant<bool, true>;
-      for (;;) {
-        if (it + 1 >= ntile) break;
-        step(NotLast{}, sa, sb);
-        if (it + 1 >= ntile) {
-  #pragma unroll
-          for (int mb = 0; mb < 2; ++mb) sa[mb] = sb[mb];
-          break;
-        }
-        step(NotLast{}, sb, sa);
-      }
-      step(Last{}, sa, sb);
+      while (it + 1 < ntile) step(NotLast{}, sc);
+      step(Last{}, sc);
     }
 
     // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
