@@ -405,24 +405,26 @@ __device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // lgkmcnt(0), serializing the operand reads of the matrix products. The
 // stage buffers' completion is waited for explicitly (wait_vmem), and the
 // "memory" clobber keeps compiler memory accesses from moving across.
+// `lds` is the LDS byte address (an integer: no generic-pointer conversion
+// and its null check per load). A load that reads M0 needs one wait state
+// after the SALU write of M0 (s_nop 0); the compiler's hazard pass does not
+// look inside inline asm.
 // Uniform base address (an SGPR pair) plus a per-lane 32-bit byte offset:
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // (The base is made visibly uniform here: it is uniform by construction, and
 // readfirstlane of a value the compiler already holds in SGPRs costs nothing.)
-__device__ inline void dma16(const void *base_any, uint32_t off, const uint8_t *lds) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(DAN_LDS const void *)lds;
+__device__ inline void dma16(const void *base_any, uint32_t off, uint32_t lds) {
   const uint64_t bv = (uint64_t)(uintptr_t)base_any;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bv), hi = __builtin_amdgcn_readfirstlane((uint32_t)(bv >> 32));
   const void *base = (const void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
-               "s"(__builtin_amdgcn_readfirstlane(m0))
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
 }
 // A per-lane 64-bit address:
-__device__ inline void dma16(const void *addr, const uint8_t *lds) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(DAN_LDS const void *)lds;
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "s"(__builtin_amdgcn_readfirstlane(m0))
+__device__ inline void dma16(const void *addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -454,9 +456,6 @@ __device__ inline const T *uniform_ptr(const T *p) {
 //    lane order. The V^T copy in the workspace has the same order, so every
 //    direct load of V^T is 1 KB of contiguous memory and every operand read
 //    is 1 KB of contiguous LDS.
-// A 1 KB sink after the buffers absorbs the direct-load slots that round the
-// per-wave load count up to a constant (only when the blocks do not divide
-// evenly among the waves).
 template <int D, int KB = 2>  // KB: bytes per K element
 struct Lds {
   static constexpr int kRowBytes = D * KB;
@@ -466,14 +465,14 @@ struct Lds {
   static constexpr int vBytes = D * kKeyTile * 2;         // fp16 V^T tile
   static constexpr int vBlocks = vBytes / 1024;
   static constexpr int blocks = kBlocks + vBlocks;
-  static constexpr int slots = (blocks + kIssuers - 1) / kIssuers;  // direct loads per issuing wave per tile
+  static_assert(kBlocks % kIssuers == 0 && vBlocks % kIssuers == 0, "blocks divide evenly among the issuing waves");
+  static constexpr int slots = blocks / kIssuers;  // direct loads per issuing wave per tile
   static constexpr int buf = kBytes + vBytes;
   // Stage buffers: a ring of four where they fit (the S product of tile j+1
   // overlaps the softmax of tile j, tile j+2 is in flight), else two (tile
   // j+1 in flight while tile j is processed: head_dim 256).
-  static constexpr int nbuf = 4 * buf + 1024 <= 160 * 1024 ? 4 : 2;
-  static constexpr int sink = nbuf * buf;
-  static constexpr int total = sink + (blocks % kIssuers ? 1024 : 0);
+  static constexpr int nbuf = 4 * buf <= 160 * 1024 ? 4 : 2;
+  static constexpr int total = nbuf * buf;
   // Swizzle: rows per 256-byte bank period, and the width of the chunk XOR.
   static constexpr int kRowsPerPeriod = kRowBytes >= 256 ? 1 : 256 / kRowBytes;
   static constexpr int kSwizzle = kChunks < 16 ? kChunks : 16;
@@ -655,6 +654,7 @@ void tree_attn_kernel(const KParams args) {
   constexpr int NC = L::kChunks;
   constexpr int RB = L::kRowBytes;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t smem_lds = (uint32_t)(uintptr_t)(DAN_LDS uint8_t *)smem;  // its LDS byte address
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -684,13 +684,14 @@ void tree_attn_kernel(const KParams args) {
   struct Src {
     const TQK *kp, *pkp;
     const _Float16 *vtp;
-    int64_t pk_st;
+    int64_t k_st, pk_st;
     int start, P, PN, ja1, jb0, ntile;
   };
   auto make_src = [&](const KParams &p, const DanUnit &un) __attribute__((always_inline)) {
     const int kvh = un.group % p.num_kv_heads;
     Src r;
     r.kp = static_cast<const TQK *>(p.k) + (int64_t)kvh * p.k_sh;
+    r.k_st = p.k_st;
     r.pkp = nullptr;
     r.pk_st = 0;
     if (un.past_len > 0) {
@@ -716,23 +717,24 @@ void tree_attn_kernel(const KParams args) {
   };
 
   // Direct-load slots. A stage buffer is kBlocks 1 KB blocks of K rows then
-  // vBlocks of V^T fragments; wave w issues blocks w, w + 8, ... (SLOTS per
-  // tile; a slot past the last block loads into the sink). K offsets are per
-  // source layout (new tokens / past) and include the row swizzle; V^T
-  // offsets are relative to the tile's block of the copy.
+  // vBlocks of V^T fragments; issuing wave w loads blocks w, w + kIssuers, ...
+  // (SLOTS per tile). Both block counts are multiples of kIssuers, so the
+  // first SK slots of every issuing wave are K blocks and the rest V^T blocks.
+  // K offsets are per source layout (new tokens / past) and include the row
+  // swizzle; V^T offsets are relative to the tile's block of the copy.
+  constexpr int SK = L::kBlocks / kIssuers;
   auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
     const int pos = blk * 64 + lane, m = pos / NC;
     const int c = (pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m);
     return (uint32_t)((k_row(m) * st + c * CE) * (int64_t)sizeof(TQK));
   };
-  uint32_t off_a[SLOTS];  // K: new-token offsets; V^T and sink: offsets in the copy
+  uint32_t off_a[SLOTS];  // K: new-token offsets; V^T: offsets in the copy
   {
     const KParams &p = *(const KParams *)kseg;
 #pragma unroll
     for (int sl = 0; sl < SLOTS; ++sl) {
       const int blk = wave + kIssuers * sl;
-      off_a[sl] = blk < L::kBlocks ? k_offset(blk, p.k_st)
-                                   : (uint32_t)((blk < L::blocks ? blk - L::kBlocks : 0) * 1024 + lane * 16);
+      off_a[sl] = sl < SK ? k_offset(blk, p.k_st) : (uint32_t)((blk - L::kBlocks) * 1024 + lane * 16);
     }
   }
   // K offsets for a prefix-cache layout of token stride st (zero elsewhere).
@@ -740,52 +742,45 @@ void tree_attn_kernel(const KParams args) {
 #pragma unroll
     for (int sl = 0; sl < SLOTS; ++sl) {
       const int blk = wave + kIssuers * sl;
-      off[sl] = blk < L::kBlocks ? k_offset(blk, st) : 0u;
+      off[sl] = sl < SK ? k_offset(blk, st) : 0u;
     }
   };
 
-  // Issue the direct loads of tile i (visit order) of source u into stage buffer b.
-  auto issue = [&](const KParams &p, const Src &u_any, const uint32_t(&off_b)[SLOTS], int i_any, int b_any)
-      __attribute__((always_inline)) {
-    // Every field is wave-uniform; saying so keeps the address arithmetic
-    // and the choice of source layout on the scalar unit (readfirstlane of a
-    // value already in SGPRs costs nothing).
-    const int i = uni(i_any), b = uni(b_any), P = uni(u_any.P), PN = uni(u_any.PN), start = uni(u_any.start);
+  // Issue the direct loads of tile i (visit order) of source u into stage
+  // buffer b: the K slots from the tile's source layout (chosen once per
+  // tile), then the V^T slots. Every field is wave-uniform; saying so keeps
+  // the address arithmetic on the scalar unit (readfirstlane of a value
+  // already in SGPRs costs nothing).
+  auto issue = [&](const Src &u_any, const uint32_t(&off_b)[SLOTS], int i_any, int b_any) __attribute__((always_inline)) {
+    const int i = uni(i_any), b = uni(b_any), P = uni(u_any.P), PN = uni(u_any.PN);
     const int ja1 = uni(u_any.ja1), jb0 = uni(u_any.jb0);
-    const TQK *ukp = uniform_ptr(u_any.kp), *upkp = uniform_ptr(u_any.pkp);
-    const int64_t pk_st = uni64(u_any.pk_st);
     const int j = i < ja1 ? i : jb0 + (i - ja1);
     const int kb = j * kKeyTile;
-    uint8_t *base = smem + b * L::buf;
-    const _Float16 *vtt = uniform_ptr(uniform_ptr(u_any.vtp) + (int64_t)j * (D * kKeyTile));
-    const int ksrc = kb + kKeyTile <= P ? 0 : (kb >= P && kb + kKeyTile <= PN) ? 1 : 2;  // past, new, straddle
-    const TQK *tb = ksrc == 0 ? uniform_ptr(upkp + (int64_t)kb * pk_st) : uniform_ptr(ukp + (int64_t)(start + kb - P) * p.k_st);
-    struct {
-      const TQK *kp, *pkp;
-      int64_t pk_st;
-      int start, P, PN;
-    } const u = {ukp, upkp, pk_st, start, P, PN};
+    const uint32_t dst = smem_lds + (uint32_t)(b * L::buf + wave * 1024);  // LDS address of slot 0; slot sl + sl * kIssuers KB
+    if (kb + kKeyTile <= P) {  // prefix-cache keys
+      const TQK *tb = uniform_ptr(uniform_ptr(u_any.pkp) + (int64_t)kb * uni64(u_any.pk_st));
 #pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl) {
-      const int blk = wave + kIssuers * sl;  // wave-uniform
-      if (blk < L::kBlocks) {
-        if (ksrc == 0) {
-          dma16(tb, off_b[sl], base + blk * 1024);
-        } else if (ksrc == 1) {
-          dma16(tb, off_a[sl], base + blk * 1024);
-        } else {  // the tile straddles the past/new boundary or the segment's end
-          const int pos = blk * 64 + lane, m = pos / NC;
-          const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
-          const int key = min(kb + k_row(m), u.PN - 1);
-          dma16(key < u.P ? u.pkp + (int64_t)key * u.pk_st + col : u.kp + (int64_t)(u.start + key - u.P) * p.k_st + col,
-                base + blk * 1024);
-        }
-      } else if (blk < L::blocks) {
-        dma16(vtt, off_a[sl], base + blk * 1024);
-      } else {
-        dma16(vtt, off_a[sl], smem + L::sink);
+      for (int sl = 0; sl < SK; ++sl) dma16(tb, off_b[sl], dst + (uint32_t)(sl * kIssuers * 1024));
+    } else if (kb >= P && kb + kKeyTile <= PN) {  // new-token keys
+      const TQK *tb = uniform_ptr(uniform_ptr(u_any.kp) + (int64_t)(uni(u_any.start) + kb - P) * uni64(u_any.k_st));
+#pragma unroll
+      for (int sl = 0; sl < SK; ++sl) dma16(tb, off_a[sl], dst + (uint32_t)(sl * kIssuers * 1024));
+    } else {  // the tile straddles the past/new boundary or the segment's end: per-lane rows
+      const TQK *kp = uniform_ptr(u_any.kp), *pkp = uniform_ptr(u_any.pkp);
+      const int64_t k_st = uni64(u_any.k_st), pk_st = uni64(u_any.pk_st);
+      const int start = uni(u_any.start);
+#pragma unroll
+      for (int sl = 0; sl < SK; ++sl) {
+        const int pos = (wave + kIssuers * sl) * 64 + lane, m = pos / NC;
+        const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
+        const int key = min(kb + k_row(m), PN - 1);
+        dma16(key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(start + key - P) * k_st + col,
+              dst + (uint32_t)(sl * kIssuers * 1024));
       }
     }
+    const _Float16 *vtt = uniform_ptr(uniform_ptr(u_any.vtp) + (int64_t)j * (D * kKeyTile));
+#pragma unroll
+    for (int sl = SK; sl < SLOTS; ++sl) dma16(vtt, off_a[sl], dst + (uint32_t)(sl * kIssuers * 1024));
   };
 
   // The stage-buffer ring runs across units: the work group's k-th tile
@@ -843,12 +838,12 @@ void tree_attn_kernel(const KParams args) {
     // Tile i of the concatenation [this unit; the next unit's first nn tiles].
     auto issue_cat = [&](int i) __attribute__((always_inline)) {
       if (i < ntile) {
-        issue(p, cur, off_b, i, (gbase + i) & (NB - 1));
+        issue(cur, off_b, i, (gbase + i) & (NB - 1));
       } else if (i - ntile < nn) {
         const Src nxt = make_src(p, load_scalar(p.units + u + 1));
         uint32_t off_nb[SLOTS];
         past_offsets(nxt.pk_st, off_nb);
-        issue(p, nxt, off_nb, i - ntile, (gbase + i) & (NB - 1));
+        issue(nxt, off_nb, i - ntile, (gbase + i) & (NB - 1));
       }
     };
     auto issued_cat = [&](int i) __attribute__((always_inline)) { return i < ntile + nn; };
@@ -1041,14 +1036,14 @@ void tree_attn_kernel(const KParams args) {
       // free), issues the next tile there and processes its own: S, mask,
       // softmax, then O += V P. The running max starts at the first tile's
       // largest visible score, as below.
-      issue(p, cur, off_b, 0, gbase & (NB - 1));
+      issue(cur, off_b, 0, gbase & (NB - 1));
       load_q(p, un);
       f32x16 s[2];
       for (int it = 0; it < ntile; ++it) {
         wait_vmem<0>();
         barrier_lds();
         const int ve = load_scalar(vexp_u + tile_of(it));
-        if (it + 1 < ntile) issue(p, cur, off_b, it + 1, (gbase + it + 1) & (NB - 1));
+        if (it + 1 < ntile) issue(cur, off_b, it + 1, (gbase + it + 1) & (NB - 1));
         qk_phase((gbase + it) & (NB - 1), s);
         mask_phase(tile_of(it), s);
         fix_straddle(tile_of(it), s);
@@ -1069,7 +1064,7 @@ void tree_attn_kernel(const KParams args) {
       if (wave < kIssuers) {
   #pragma unroll
         for (int t = 0; t < 3; ++t)
-          if (t >= pre && t < ntile) issue(p, cur, off_b, t, (gbase + t) & (NB - 1));
+          if (t >= pre && t < ntile) issue(cur, off_b, t, (gbase + t) & (NB - 1));
         for (int t = ntile; t < 3; ++t) issue_cat(t);
       }
       if (!q_ready) load_q(p, un);
