@@ -457,7 +457,8 @@ def _gdn_layer_times(args, w, hk, hv, d, dev, hidden=2048, kernel=4):
     from types import SimpleNamespace
 
     from dan_amd.attention import Batch
-    from dan_amd.deltanet import DeltaNet, RecurrentLayout, conv_phase
+    from dan_amd import _native
+    from dan_amd.deltanet import DeltaNet, RecurrentLayout, conv_phase_args
 
     cfg = SimpleNamespace(linear_num_key_heads=hk, linear_num_value_heads=hv, linear_key_head_dim=d,
                           linear_value_head_dim=d, linear_conv_kernel_dim=kernel, hidden_size=hidden,
@@ -480,7 +481,12 @@ def _gdn_layer_times(args, w, hk, hv, d, dev, hidden=2048, kernel=4):
         ba = torch.randn(n, 2 * hv, device=dev, generator=g).to(torch.bfloat16)
         hist = torch.cat([segs[i].past[0][0] for i in segs.recurrent.past_segments]) if segs.recurrent.past_segments else None
         ph = segs.recurrent.trunk1
-        fn = lambda: conv_phase(qkv, hist, ph, m.conv1d.weight, ba[:, :hv], ba[:, hv:], m.A_log, m.dt_bias)
+        # The phase's arguments built once and the library called directly, so the
+        # timing is the launches' (the Python wrapper's per-call set-up costs about as
+        # much as the kernels).
+        cx, _, keep = conv_phase_args(qkv, hist, ph, m.conv1d.weight, ba[:, :hv], ba[:, hv:], m.A_log, m.dt_bias)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        fn = lambda: _native.gdn_conv(cx, stream)
         fn()
         conv_ms = _event_ms(fn, args.steps)
     t = len(ph.rows)

@@ -6,10 +6,12 @@
 //   gdn_conv_kernel   one thread per (strip of kStrip output rows, 8 channels).
 //                     Consecutive threads take consecutive 16-byte channel
 //                     groups of the same rows, so every row load is coalesced.
-//                     Along a strip the K-row window slides: output row i + 1
-//                     of a run starts one ext entry after row i, so one new
-//                     row is loaded per output row and a full window only at a
-//                     run boundary. Sum in fp32 (j = 0 .. K-1, fused
+//                     A strip's window starts, ext entries and rows are each
+//                     loaded as one batch (all in flight), not one memory
+//                     round trip per row. Along a strip the K-row window
+//                     slides: output row i + 1 of a run starts one ext entry
+//                     after row i, so one new row is loaded per output row
+//                     and a full window only at a run boundary. Sum in fp32 (j = 0 .. K-1, fused
 //                     multiply-adds), rounded to the I/O type as the
 //                     reference's conv1d output is, then silu in fp32 (hardware
 //                     exp2 and reciprocal: the kernel is otherwise VALU-bound
@@ -30,7 +32,7 @@ extern thread_local char g_err[512];
 
 namespace dan_conv {
 
-constexpr int kStrip = 16;  // output rows per thread
+constexpr int kStrip = 8;  // output rows per thread (16 held too many loads' registers: 2 waves per SIMD)
 constexpr int kBlock = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -88,27 +90,15 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
   const int cg = (int)(gid % p.groups);
   const int64_t i0 = gid / p.groups * kStrip;
   if (i0 >= p.T) return;
-  const int i1 = (int)min((int64_t)p.T, i0 + kStrip);
+  const int nr = (int)min((int64_t)p.T - i0, (int64_t)kStrip);  // output rows of this strip
   f32x8 w[K];
   const T *wp = static_cast<const T *>(p.weight) + (int64_t)cg * 8 * K;
 #pragma unroll
   for (int c = 0; c < 8; ++c)
 #pragma unroll
     for (int j = 0; j < K; ++j) w[j][c] = (float)wp[c * K + j];
-  f32x8 x[K];
-  int prev = -2;  // window start of the previous output row
-  for (int i = (int)i0; i < i1; ++i) {
-    int t = p.take[i];
-    if (t < 0 || t > p.num_ext - K) t = -1;  // out of range: the window reads as zeros
-    if (t >= 0 && t == prev + 1) {
-#pragma unroll
-      for (int j = 0; j < K - 1; ++j) x[j] = x[j + 1];
-      x[K - 1] = load_row<T>(p, p.ext[t + K - 1], cg);
-    } else {
-#pragma unroll
-      for (int j = 0; j < K; ++j) x[j] = t >= 0 ? load_row<T>(p, p.ext[t + j], cg) : f32x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-    prev = t >= 0 ? t : -2;  // no slide out of a zero window
+  T *out = static_cast<T *>(p.out) + i0 * p.out_stride + 8 * cg;
+  auto emit = [&](int r, const f32x8(&x)[K]) __attribute__((always_inline)) {
     f32x8 y;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -120,7 +110,76 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
       // one fp32 ulp each, far below the output type's spacing)
       y[c] = r * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(r * -1.4426950408889634f));
     }
-    *(DAN_GLOBAL u32x4 *)(static_cast<T *>(p.out) + (int64_t)i * p.out_stride + 8 * cg) = pack8<T>(y);
+    *(DAN_GLOBAL u32x4 *)(out + (int64_t)r * p.out_stride) = pack8<T>(y);
+  };
+  // With no source row or too few ext entries every window reads as zeros.
+  if (!((p.N > 0 || p.hist_rows > 0) && p.num_ext >= K)) {
+    f32x8 x[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) x[j] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int r = 0; r < nr; ++r) emit(r, x);
+    return;
+  }
+  // Virtual source row e: a packed row, a history row, or zeros. Every load is
+  // issued unconditionally -- a zero row reads a row that exists (packed row
+  // 0, else history row 0) and is masked -- so a strip's loads are in flight
+  // together instead of one memory round trip per branch.
+  const T *src = static_cast<const T *>(p.src), *hist = static_cast<const T *>(p.hist);
+  const T *stand = p.N > 0 ? src : hist;
+  auto row_at = [&](int e, bool &ok) __attribute__((always_inline)) {
+    const bool in_src = e >= 0 && e < p.N, in_hist = e > p.N && e - p.N - 1 < p.hist_rows;
+    ok = in_src || in_hist;
+    const T *row = in_src ? src + (int64_t)e * p.src_stride : in_hist ? hist + (int64_t)(e - p.N - 1) * p.C : stand;
+    return *(const DAN_GLOBAL u32x4 *)(row + 8 * cg);
+  };
+  // 1. The strip's window starts (rows past the strip repeat its last row and
+  //    are not stored). A start outside [0, num_ext - K] reads as zeros.
+  int t[kStrip];
+  bool tv[kStrip];
+#pragma unroll
+  for (int r = 0; r < kStrip; ++r) t[r] = p.take[i0 + min(r, nr - 1)];
+#pragma unroll
+  for (int r = 0; r < kStrip; ++r) {
+    tv[r] = t[r] >= 0 && t[r] <= p.num_ext - K;
+    t[r] = tv[r] ? t[r] : 0;
+  }
+  // 2. Each row's newest window entry, and the first row's older ones.
+  int en[kStrip], ep[K - 1];
+#pragma unroll
+  for (int r = 0; r < kStrip; ++r) en[r] = p.ext[t[r] + K - 1];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) ep[j] = p.ext[t[0] + j];
+  // 3. Their rows.
+  u32x4 rn[kStrip], rp[K - 1];
+  bool okn[kStrip], okp[K - 1];
+#pragma unroll
+  for (int r = 0; r < kStrip; ++r) rn[r] = row_at(en[r], okn[r]);
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) rp[j] = row_at(ep[j], okp[j]);
+  const f32x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  // 4. The outputs. Along a run the window slides one entry per output row;
+  //    at a run boundary (rare) the row's older entries are loaded then.
+  f32x8 x[K];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) x[j] = tv[0] && okp[j] ? cvt8<T>(rp[j]) : zero;
+  x[K - 1] = tv[0] && okn[0] ? cvt8<T>(rn[0]) : zero;
+  emit(0, x);
+#pragma unroll
+  for (int r = 1; r < kStrip; ++r) {
+    // (rows past nr repeat the strip's last row: computed, not stored)
+    if (tv[r] && tv[r - 1] && t[r] == t[r - 1] + 1) {
+#pragma unroll
+      for (int j = 0; j < K - 1; ++j) x[j] = x[j + 1];
+    } else {
+#pragma unroll
+      for (int j = 0; j < K - 1; ++j) {
+        bool ok = false;
+        const u32x4 raw = tv[r] ? row_at(p.ext[t[r] + j], ok) : u32x4{0, 0, 0, 0};
+        x[j] = ok ? cvt8<T>(raw) : zero;
+      }
+    }
+    x[K - 1] = tv[r] && okn[r] ? cvt8<T>(rn[r]) : zero;
+    if (r < nr) emit(r, x);
   }
 }
 

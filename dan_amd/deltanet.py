@@ -216,6 +216,15 @@ def conv_phase(qkv, hist, ph, weight, b, a, a_log, dt_bias):
     histories in layout order or None, ``weight`` [C, 1, K], ``b``/``a``
     [N, Hv], ``a_log``/``dt_bias`` [Hv]. Returns (conv [T, C] in qkv's dtype,
     beta [T, Hv] fp32, g [T, Hv] fp32)."""
+    x, outs, _keep = conv_phase_args(qkv, hist, ph, weight, b, a, a_log, dt_bias)
+    _native.gdn_conv(x, torch.cuda.current_stream(qkv.device).cuda_stream)
+    return outs
+
+
+def conv_phase_args(qkv, hist, ph, weight, b, a, a_log, dt_bias):
+    """``conv_phase``'s ``DanGdnConvArgs``, its outputs (conv, beta, g) and the
+    tensors the arguments point at (keep them alive while the call runs), so
+    that a caller can launch the same phase again without rebuilding them."""
     if not qkv.is_cuda:
         raise RuntimeError("dan_amd.deltanet.conv_phase runs on a gfx950 GPU only")
     n, c = qkv.shape
@@ -246,8 +255,7 @@ def conv_phase(qkv, hist, ph, weight, b, a, a_log, dt_bias):
     x.num_heads, x.rows = hv, ph.rows.data_ptr()
     x.b, x.b_stride, x.a, x.a_stride = b.data_ptr(), b.stride(0), a.data_ptr(), a.stride(0)
     x.a_log, x.dt_bias, x.beta, x.g = al.data_ptr(), dtb.data_ptr(), beta.data_ptr(), g.data_ptr()
-    _native.gdn_conv(x, torch.cuda.current_stream(dev).cuda_stream)
-    return out, beta, g
+    return x, (out, beta, g), (qkv, w, hist, b, a, al, dtb, ph)
 
 
 class DeltaNet(nn.Module):

@@ -89,6 +89,63 @@ def test_conv_phase_matches_oracle(gpu, dtype):
         assert ((gg.cpu() - rg[rows]).abs() <= 2e-6 * rg[rows].abs() + 1e-7).all()
 
 
+
+@pytest.mark.parametrize("kernel", [2, 3, 4])
+@pytest.mark.parametrize("n_rows, n_hist, n_ext, n_out, mode",
+                         [(300, 3, 320, 251, "runs"), (120, 0, 130, 37, "wild"), (0, 5, 12, 21, "runs"),
+                          (64, 2, 80, 1, "runs"), (17, 1, 3, 20, "wild")])
+def test_conv_table_edges(gpu, kernel, n_rows, n_hist, n_ext, n_out, mode):
+    """dan_gdn_conv on hand-made tables: runs whose boundaries fall inside a
+    thread's strip of output rows, a ragged last strip, window starts and ext
+    entries outside their ranges (zero windows and zero rows), no packed rows,
+    and fewer ext entries than a window. Against silu_conv over the virtual
+    source the ABI defines (packed row e, zeros at e == N, history row
+    e - N - 1, zeros elsewhere)."""
+    dtype, c, hv = torch.bfloat16, 64, 2
+    say(f"conv table K {kernel} N {n_rows} hist {n_hist} ext {n_ext} T {n_out} {mode}")
+    g = torch.Generator().manual_seed(11 + kernel + n_out)
+    proj = torch.randn(max(n_rows, 1), c + 16, generator=g).to(dtype)
+    hist = torch.randn(max(n_hist, 1), c, generator=g).to(dtype)
+    top = n_rows + 1 + n_hist
+    ext = torch.randint(-3, top + 4, (n_ext,), generator=g, dtype=torch.int32)
+    if mode == "runs":
+        take = []
+        while len(take) < n_out:
+            run = int(torch.randint(1, 13, (1,), generator=g))
+            first = int(torch.randint(0, max(n_ext - kernel - run + 2, 1), (1,), generator=g))
+            take += [first + i for i in range(run)]  # may run past the last valid start
+        take = torch.tensor(take[:n_out], dtype=torch.int32)
+    else:
+        take = torch.randint(-3, n_ext + 2, (n_out,), generator=g, dtype=torch.int32)
+    w = (torch.randn(c, 1, kernel, generator=g) * 0.5).to(dtype)
+    b = torch.randn(max(n_rows, 1), hv, generator=g).to(dtype)
+    a = torch.randn(max(n_rows, 1), hv, generator=g).to(dtype)
+    rows = torch.randint(-1, max(n_rows, 1) + 1, (n_out,), generator=g, dtype=torch.int32)
+    ph = SimpleNamespace(rows=rows.to(gpu), ext=ext.to(gpu), take=take.to(gpu))
+    src = proj[:n_rows, :c].to(gpu)
+    out, _, _ = conv_phase(src, hist[:n_hist].to(gpu) if n_hist else None, ph, w.to(gpu), b.to(gpu), a.to(gpu),
+                           torch.randn(hv, generator=g).to(gpu), torch.randn(hv, generator=g).to(gpu))
+    torch.cuda.synchronize()
+
+    def virtual(e):
+        if 0 <= e < n_rows:
+            return proj[e, :c]
+        if n_rows < e <= n_rows + n_hist:
+            return hist[e - n_rows - 1]
+        return torch.zeros(c, dtype=dtype)
+
+    ref = []
+    for t in take.tolist():
+        if 0 <= t <= n_ext - kernel:
+            win = torch.stack([virtual(int(ext[t + j])) for j in range(kernel)])
+        else:
+            win = torch.zeros(kernel, c, dtype=dtype)
+        ref.append(D.silu_conv(win, w[:, 0])[0])
+    ref = torch.stack(ref).double()
+    e = (out.cpu().double() - ref).abs()
+    say(f"  max |conv - ref| {e.max().item():.3e}")
+    assert (e <= 2.0 ** -7 * ref.abs() + 1e-30).all()
+
 def test_layer_matches_oracle(gpu):
     w = weights(11)
     segs, x = tree_batch(12)
