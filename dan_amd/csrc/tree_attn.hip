@@ -881,7 +881,7 @@ void tree_attn_kernel(const KParams args) {
     u32x4 pf[4];  // P^T B operands (fp16), one per 16 keys of the tile
 
     // S^T = K Q^T for the 64 keys of stage buffer b x this wave's 32 queries.
-    auto qk_phase = [&](int b, f32x16(&s)[2]) {
+    auto qk_phase = [&](int b, f32x16(&s)[2], auto &&after_kstep) {
       // LDS address of this lane's row in buffer b. The dynamic LDS block is
       // the kernel's only LDS object and starts at address 0, and buffer
       // offsets are multiples of 32 rows, so XOR-ing a chunk into the address
@@ -901,6 +901,7 @@ void tree_attn_kernel(const KParams args) {
         }
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) s[mb] = mfma_qk<TQK>(a[mb], qf[kk], s[mb]);
+        after_kstep(kk);
       }
     };
     // Tree mask on boundary tiles. Key index of register r relative to the tile
@@ -1043,8 +1044,32 @@ void tree_attn_kernel(const KParams args) {
         wait_vmem<0>();
         barrier_lds();
         const int ve = load_scalar(vexp_u + tile_of(it));
-        if (it + 1 < ntile) issue(cur, off_b, it + 1, (gbase + it + 1) & (NB - 1));
-        qk_phase((gbase + it) & (NB - 1), s);
+        // The next tile's loads go out one slot per k-step of this tile's S
+        // (a wave alone on its SIMD would otherwise stall on the burst); a
+        // tile straddling the past/new boundary issues them all now.
+        int kind = 2;
+        const TQK *sp_tb = cur.kp;
+        const _Float16 *sp_vtt = cur.vtp;
+        uint32_t sp_dst = 0;
+        if (it + 1 < ntile) {
+          const int i = it + 1, j = tile_of(i), kb = j * kKeyTile;
+          kind = kb + kKeyTile <= P ? 0 : (kb >= P && kb + kKeyTile <= cur.PN) ? 1 : 2;
+          sp_tb = kind == 0 ? cur.pkp + (int64_t)kb * cur.pk_st : cur.kp + (int64_t)(cur.start + kb - P) * cur.k_st;
+          sp_vtt = cur.vtp + (int64_t)j * (D * kKeyTile);
+          sp_dst = smem_lds + (uint32_t)(((gbase + i) & (NB - 1)) * L::buf + wave * 1024);
+          if (kind == 2) issue(cur, off_b, i, (gbase + i) & (NB - 1));
+        }
+        if (kind != 2) {
+          qk_phase((gbase + it) & (NB - 1), s, [&](int kk) __attribute__((always_inline)) {
+#pragma unroll
+            for (int sl = kk * SLOTS / NK; sl < (kk + 1) * SLOTS / NK; ++sl) {
+              if (sl < SK) dma16(sp_tb, kind == 0 ? off_b[sl] : off_a[sl], sp_dst + (uint32_t)(sl * kIssuers * 1024));
+              else dma16(sp_vtt, off_a[sl], sp_dst + (uint32_t)(sl * kIssuers * 1024));
+            }
+          });
+        } else {
+          qk_phase((gbase + it) & (NB - 1), s, [](int) {});
+        }
         mask_phase(tile_of(it), s);
         fix_straddle(tile_of(it), s);
         const float c = tile_c(tile_of(it));
@@ -1079,7 +1104,7 @@ void tree_attn_kernel(const KParams args) {
       // first visible key scores far above m + kLog2Limit, which raises m to
       // that tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0).
       // Finite throughout, so no inf - inf.
-      qk_phase(gbase & (NB - 1), sc);
+      qk_phase(gbase & (NB - 1), sc, [](int) {});
       mask_phase(tile_of(0), sc);
       fix_straddle(tile_of(0), sc);
       mneg = -fmaxf(s_max(sc) * tile_c(tile_of(0)), -3.0e38f);
@@ -1110,7 +1135,7 @@ void tree_attn_kernel(const KParams args) {
         const float c = tile_c(tile_of(it));
         begin_tile(s, c, ve);
         const float ts = exp_phase(s, c);
-        if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), s);
+        if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), s, [](int) {});
         lsum += ts;
         pv_phase((gbase + it) & (NB - 1));
         if (!kLast) {
