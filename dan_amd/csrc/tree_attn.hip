@@ -554,20 +554,20 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const PackParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t tile[D * 32];
   __shared__ float wave_max[4];
   const int kvh = blockIdx.x % p.num_kv_heads, cb = blockIdx.x / p.num_kv_heads;
-  if (p.counts && cb >= *gbl(p.counts + 3)) return;  // past this batch's columns (the grid covers the capacity)
-  const DanSegmentDesc sg = load_entry(p.segs + *gbl(p.col_seg + cb));
+  if (p.counts && cb >= load_scalar(p.counts + 3)) return;  // past this batch's columns (the grid covers the capacity)
+  const DanSegmentDesc sg = load_scalar(p.segs + load_scalar(p.col_seg + cb));
   const int key0 = cb * kKeyTile - sg.vt_col;
   const int P = sg.past_len, PN = P + sg.n;
   const TV *vp = static_cast<const TV *>(p.v) + (int64_t)kvh * p.v_sh;
   const TV *pvp = nullptr;
   int64_t pv_st = 0;
   float vs = 1.f, pvs = 1.f;
-  if (kF8) vs = *gbl(p.v_scale);
+  if (kF8) vs = load_scalar(p.v_scale);
   if (P > 0) {
-    const DanPastDesc pd = load_entry(p.pasts + sg.past_idx);
+    const DanPastDesc pd = load_scalar(p.pasts + sg.past_idx);
     pvp = static_cast<const TV *>(pd.v) + (int64_t)kvh * pd.v_stride_head;
     pv_st = pd.v_stride_tok;
-    if (kF8) pvs = *gbl(pd.v_scale);
+    if (kF8) pvs = load_scalar(pd.v_scale);
   }
   // 8 values of key `key` (segment key coordinates) from d chunk c, as fp32.
   // Branch-free: a key past the segment reads a stand-in row (the segment's
