@@ -889,6 +889,25 @@ void tree_attn_kernel(const KParams args) {
       const uint32_t kbase = (uint32_t)(uintptr_t)(DAN_LDS uint8_t *)(smem + b * L::buf) + k_lane;
       s[0] = f32x16{};
       s[1] = f32x16{};
+      if constexpr (kTwoStage) {
+        Frag<TQK> a[NK][2];
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            const uint32_t off = kbase ^ (uint32_t)((2 * kk * CH + i) * 16);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+              a[kk][mb].c[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(off + mb * 32 * RB));
+          }
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) {
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) s[mb] = mfma_qk<TQK>(a[kk][mb], qf[kk], s[mb]);
+          after_kstep(kk);
+        }
+        return;
+      }
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         Frag<TQK> a[2];
@@ -1019,6 +1038,18 @@ void tree_attn_kernel(const KParams args) {
     // O's scale: begin_tile).
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
       const uint8_t *vbuf = smem + b * L::buf + v_lane;
+      if constexpr (kTwoStage) {
+        u32x4 a[4][ND];
+#pragma unroll
+        for (int kj = 0; kj < 4; ++kj)
+#pragma unroll
+          for (int db = 0; db < ND; ++db) a[kj][db] = *reinterpret_cast<const u32x4 *>(vbuf + (kj * ND + db) * 1024);
+#pragma unroll
+        for (int kj = 0; kj < 4; ++kj)
+#pragma unroll
+          for (int db = 0; db < ND; ++db) o[db] = mfma32<_Float16>(a[kj][db], pf[kj], o[db]);
+        return;
+      }
 #pragma unroll
       for (int kj = 0; kj < 4; ++kj) {
 #pragma unroll
