@@ -78,6 +78,24 @@ __device__ inline void store16(T *p, u32x4 v) {
   *(DAN_GLOBAL u32x4 *)p = v;
 }
 
+// Lane l's value from lane l ^ 1 / l ^ 2 of its quad, lane 7 - l of its
+// 8-lane half-row, lane 15 - l of its 16-lane row (DPP: no LDS round trip).
+#define DAN_DPP(x, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
+// The sum of v over the L lanes of a head vector (L = 8, 16 or 32 consecutive
+// lanes from a multiple of L), in every one of them. Once a quad holds its sum
+// in every lane, the half-row mirror reads the other quad of the half-row and
+// the row mirror the other half of the row, so each step adds the same pair
+// as an xor butterfly over lane ^ 1, ^ 2, ^ 4, ^ 8 (^ 16 across rows).
+template <int L>
+__device__ inline float vec_sum(float v) {
+  v += DAN_DPP(v, 0xB1);   // quad_perm 1, 0, 3, 2
+  v += DAN_DPP(v, 0x4E);   // quad_perm 2, 3, 0, 1
+  v += DAN_DPP(v, 0x141);  // row_half_mirror
+  if constexpr (L >= 16) v += DAN_DPP(v, 0x140);  // row_mirror
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 32);
+  return v;
+}
+
 struct Params {
   const void *q, *k, *v, *cos, *sin, *qw, *kw;
   void *qo, *ko;
@@ -120,8 +138,7 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-#pragma unroll
-    for (int m = 1; m < L; m <<= 1) ss += __shfl_xor(ss, m, L);
+    ss = vec_sum<L>(ss);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
