@@ -111,13 +111,22 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
   __shared__ float sL[kC][kC + 4];
   __shared__ float sG[kC];
   const int s = blockIdx.x / p.Hv, h = blockIdx.x % p.Hv;
-  int lo = 0, hi = p.R - 1;  // the run of slot s: the largest r with slot_of(r) <= s
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (slot_of(p.cu, mid) <= s) lo = mid;
-    else hi = mid - 1;
+  // The run of slot s: the largest r with slot_of(r) <= s. slot_of increases
+  // strictly with r (slot_of(0) = 0), so r + 1 is the number of runs whose
+  // slot is at most s: each wave counts them 64 runs at a time with one load
+  // per lane, all in flight, instead of a binary search's chain of loads.
+  int r = 0;
+  {
+    const int ln = threadIdx.x & 63;
+    for (int base = 0; base < p.R; base += 64) {
+      const int rr = base + ln;
+      const bool le = rr < p.R && slot_of(p.cu, min(rr, p.R - 1)) <= s;
+      const uint64_t m = __ballot(le);
+      r = base + __popcll(m) - 1;
+      if (m != ~0ull) break;  // a run of this block starts past s (or the runs end here)
+    }
+    r = max(r, 0);
   }
-  const int r = lo;
   const int t0 = *(const DAN_GLOBAL int32_t *)(p.cu + r) + kC * (s - slot_of(p.cu, r));
   const int end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
   if (t0 >= end) return;  // the whole group, before any barrier
