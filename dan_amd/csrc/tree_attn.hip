@@ -890,9 +890,13 @@ void tree_attn_kernel(const KParams args) {
       s[0] = f32x16{};
       s[1] = f32x16{};
       if constexpr (kTwoStage) {
+        // Operand fragments are read W = 2 k-steps ahead of their products.
+        // Reading all NK first (128 VGPRs at bf16) spilled O-side registers
+        // to scratch inside the tile loop; two k-steps keep the matrix core
+        // fed with no spill.
+        constexpr int W = NK < 2 ? NK : 2;
         Frag<TQK> a[NK][2];
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk)
+        auto rd = [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
           for (int i = 0; i < CH; ++i) {
             const uint32_t off = kbase ^ (uint32_t)((2 * kk * CH + i) * 16);
@@ -900,8 +904,12 @@ void tree_attn_kernel(const KParams args) {
             for (int mb = 0; mb < 2; ++mb)
               a[kk][mb].c[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(off + mb * 32 * RB));
           }
+        };
+#pragma unroll
+        for (int kk = 0; kk < W; ++kk) rd(kk);
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) {
+          if (kk + W < NK) rd(kk + W);
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb) s[mb] = mfma_qk<TQK>(a[kk][mb], qf[kk], s[mb]);
           after_kstep(kk);
@@ -1039,15 +1047,20 @@ void tree_attn_kernel(const KParams args) {
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
       const uint8_t *vbuf = smem + b * L::buf + v_lane;
       if constexpr (kTwoStage) {
+        // V^T fragments two key groups (of four) ahead of their products.
         u32x4 a[4][ND];
-#pragma unroll
-        for (int kj = 0; kj < 4; ++kj)
+        auto rd = [&](int kj) __attribute__((always_inline)) {
 #pragma unroll
           for (int db = 0; db < ND; ++db) a[kj][db] = *reinterpret_cast<const u32x4 *>(vbuf + (kj * ND + db) * 1024);
+        };
+        rd(0);
+        rd(1);
 #pragma unroll
-        for (int kj = 0; kj < 4; ++kj)
+        for (int kj = 0; kj < 4; ++kj) {
+          if (kj + 2 < 4) rd(kj + 2);
 #pragma unroll
           for (int db = 0; db < ND; ++db) o[db] = mfma32<_Float16>(a[kj][db], pf[kj], o[db]);
+        }
         return;
       }
 #pragma unroll
