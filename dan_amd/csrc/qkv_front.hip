@@ -106,87 +106,123 @@ struct Params {
   float eps;
 };
 
+// Head vectors per lane (qkv_front_kernel).
+constexpr int kVecs = 2;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
   constexpr int L = D / 8;      // lanes per head vector
-  constexpr int VPB = 256 / L;  // head vectors per work group
+  constexpr int VPB = 256 / L;  // head vectors per work group and pass
   const int slot = threadIdx.x / L, j = threadIdx.x % L;
   const int HV = p.H + p.Hkv;
-  const int64_t vi = (int64_t)blockIdx.x * VPB + slot;
+  // A lane takes kVecs head vectors VPB apart, all loaded before any math, so
+  // a wave keeps twice the bytes in flight through the norm's reduction.
+  const int64_t v0 = (int64_t)blockIdx.x * (kVecs * VPB) + slot;
   // Whole vectors (all L lanes of one) leave together, so the lane
-  // exchanges below only ever involve lanes of a live vector.
-  if (vi >= (int64_t)p.N * HV) return;
-  const int t = (int)(vi / HV), hv = (int)(vi % HV);
-  const bool isq = hv < p.H;
-  const int head = isq ? hv : hv - p.H;
-  const T *src = isq ? static_cast<const T *>(p.q) + t * p.q_st + head * p.q_sh
-                     : static_cast<const T *>(p.k) + t * p.k_st + head * p.k_sh;
-  // Every operand is loaded here, unconditionally (a stand-in row, the lane's
-  // own x, where the norm weight or the rotary tables are unused): loads
-  // under branches would make the compiler wait for each one in turn.
-  const T *row = src + 8 * j;
-  const T *wrow = p.norm != DAN_FRONT_NORM_NONE ? static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j : row;
-  const int64_t cs_off = (int64_t)t * p.cs_st + min(8 * j, p.R - 8);
-  const T *crow = p.R > 0 ? static_cast<const T *>(p.cos) + cs_off : row;
-  const T *srow = p.R > 0 ? static_cast<const T *>(p.sin) + cs_off : row;
-  const u32x4 xraw = load16(row), wraw = load16(wrow), craw = load16(crow), sraw = load16(srow);
-  __builtin_amdgcn_sched_barrier(0);  // the scheduler would issue the weight load after the norm's math
-  const f32x8 x = to_f32<T>(xraw), w = to_f32<T>(wraw), cs = to_f32<T>(craw), sn = to_f32<T>(sraw);
-
-  f32x8 n = x;
-  if (p.norm != DAN_FRONT_NORM_NONE) {
-    float ss = 0.f;
+  // exchanges below only ever involve lanes of a live vector. A later vector
+  // past the end is computed on a stand-in (the last vector) and not stored.
+  if (v0 >= (int64_t)p.N * HV) return;
+  int tv[kVecs], headv[kVecs];
+  bool isqv[kVecs], okv[kVecs];
+  u32x4 xraw[kVecs], wraw[kVecs], craw[kVecs], sraw[kVecs];
+  {
+    int t = (int)(v0 / HV), hv = (int)(v0 % HV);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-    ss = vec_sum<L>(ss);
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float y = x[i] * r;
-      n[i] = p.norm == DAN_FRONT_NORM_RMS ? rnd<T>(w[i] * rnd<T>(y)) : rnd<T>(y * (1.0f + w[i]));
+    for (int k = 0; k < kVecs; ++k) {
+      bool ok = true;
+      if (k > 0) {
+        hv += VPB;
+        t += hv / HV;
+        hv %= HV;
+        ok = t < p.N;
+      }
+      const int tc = ok ? t : p.N - 1, hc = ok ? hv : HV - 1;
+      const bool isq = hc < p.H;
+      const int head = isq ? hc : hc - p.H;
+      tv[k] = tc;
+      headv[k] = head;
+      isqv[k] = isq;
+      okv[k] = ok;
+      const T *src = isq ? static_cast<const T *>(p.q) + tc * p.q_st + head * p.q_sh
+                         : static_cast<const T *>(p.k) + tc * p.k_st + head * p.k_sh;
+      // Every operand is loaded here, unconditionally (a stand-in row, the
+      // lane's own x, where the norm weight or the rotary tables are unused):
+      // loads under branches would make the compiler wait for each in turn.
+      const T *row = src + 8 * j;
+      const T *wrow = p.norm != DAN_FRONT_NORM_NONE ? static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j : row;
+      const int64_t cs_off = (int64_t)tc * p.cs_st + min(8 * j, p.R - 8);
+      const T *crow = p.R > 0 ? static_cast<const T *>(p.cos) + cs_off : row;
+      const T *srow = p.R > 0 ? static_cast<const T *>(p.sin) + cs_off : row;
+      xraw[k] = load16(row);
+      wraw[k] = load16(wrow);
+      craw[k] = load16(crow);
+      sraw[k] = load16(srow);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // the scheduler would issue the weight loads after the norm's math
 
-  f32x8 o = n;
-  if (8 * j < p.R) {
-    const int half = p.R / 16;  // lanes per rotary half
-    const int partner = j < half ? j + half : j - half;
-    const u32x4 np = from_f32<T>(n);  // exact: n is already rounded to T
-    u32x4 pp;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t word = np[c];
-      pp[c] = (uint32_t)__shfl((int)word, partner, L);  // lane `partner` of this vector's L lanes
-    }
-    const f32x8 pv = to_f32<T>(pp);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float rot = j < half ? -pv[i] : pv[i];
-      o[i] = rnd<T>(rnd<T>(n[i] * cs[i]) + rnd<T>(rot * sn[i]));
-    }
-  }
-  const u32x4 out = from_f32<T>(o);
-  T *dst = isq ? static_cast<T *>(p.qo) + t * p.qo_st + head * p.qo_sh
-               : static_cast<T *>(p.ko) + t * p.ko_st + head * p.ko_sh;
-  store16(dst + 8 * j, out);
+  for (int k = 0; k < kVecs; ++k) {
+    const int t = tv[k], head = headv[k];
+    const bool isq = isqv[k];
+    const f32x8 x = to_f32<T>(xraw[k]), w = to_f32<T>(wraw[k]), cs = to_f32<T>(craw[k]), sn = to_f32<T>(sraw[k]);
 
-  // Prefix save: the kv-head vector of a saved token also writes its k row
-  // and copies its v row.
-  if (!isq && p.save_of) {
-    const int si = p.save_of[t];
-    if (si >= 0) {
-      const DanFrontSave sv = p.saves[si];
-      const int64_t row = (int64_t)head * sv.len + (t - sv.start);
-      store16(static_cast<T *>(sv.k_dst) + row * D + 8 * j, out);
-      const T *vs = static_cast<const T *>(p.v) + t * p.v_st + head * p.v_sh;
-      store16(static_cast<T *>(sv.v_dst) + row * D + 8 * j, load16(vs + 8 * j));
+    f32x8 n = x;
+    if (p.norm != DAN_FRONT_NORM_NONE) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+      ss = vec_sum<L>(ss);
+      const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float y = x[i] * r;
+        n[i] = p.norm == DAN_FRONT_NORM_RMS ? rnd<T>(w[i] * rnd<T>(y)) : rnd<T>(y * (1.0f + w[i]));
+      }
+    }
+
+    f32x8 o = n;
+    if (8 * j < p.R) {
+      const int half = p.R / 16;  // lanes per rotary half
+      const int partner = j < half ? j + half : j - half;
+      const u32x4 np = from_f32<T>(n);  // exact: n is already rounded to T
+      u32x4 pp;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t word = np[c];
+        pp[c] = (uint32_t)__shfl((int)word, partner, L);  // lane `partner` of this vector's L lanes
+      }
+      const f32x8 pv = to_f32<T>(pp);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float rot = j < half ? -pv[i] : pv[i];
+        o[i] = rnd<T>(rnd<T>(n[i] * cs[i]) + rnd<T>(rot * sn[i]));
+      }
+    }
+    if (!okv[k]) continue;
+    const u32x4 out = from_f32<T>(o);
+    T *dst = isq ? static_cast<T *>(p.qo) + t * p.qo_st + head * p.qo_sh
+                 : static_cast<T *>(p.ko) + t * p.ko_st + head * p.ko_sh;
+    store16(dst + 8 * j, out);
+
+    // Prefix save: the kv-head vector of a saved token also writes its k row
+    // and copies its v row.
+    if (!isq && p.save_of) {
+      const int si = p.save_of[t];
+      if (si >= 0) {
+        const DanFrontSave sv = p.saves[si];
+        const int64_t row = (int64_t)head * sv.len + (t - sv.start);
+        store16(static_cast<T *>(sv.k_dst) + row * D + 8 * j, out);
+        const T *vs = static_cast<const T *>(p.v) + t * p.v_st + head * p.v_sh;
+        store16(static_cast<T *>(sv.v_dst) + row * D + 8 * j, load16(vs + 8 * j));
+      }
     }
   }
 }
 
 template <typename T, int D>
 hipError_t launch(const Params &p, hipStream_t s) {
-  constexpr int VPB = 256 / (D / 8);
+  constexpr int VPB = kVecs * (256 / (D / 8));  // head vectors per work group
   const int64_t vectors = (int64_t)p.N * (p.H + p.Hkv);
   const int64_t grid = (vectors + VPB - 1) / VPB;
   hipLaunchKernelGGL((qkv_front_kernel<T, D>), dim3((unsigned)grid), dim3(256), 0, s, p);
