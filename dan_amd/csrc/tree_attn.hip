@@ -891,7 +891,7 @@ void tree_attn_kernel(const KParams args) {
       s[1] = f32x16{};
       if constexpr (kTwoStage) {
         // Operand fragments are read W = 2 k-steps ahead of their products.
-        // Reading all NK first (128 VGPRs at bf16) spilled O-side registers
+        // Reading all NK first (128 VGPRs at bf16) made the compiler spill
         // to scratch inside the tile loop; two k-steps keep the matrix core
         // fed with no spill.
         constexpr int W = NK < 2 ? NK : 2;
