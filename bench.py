@@ -509,7 +509,8 @@ def bench_plan(args):
     dev = torch.device("cuda:0")
     w = {**workloads.CONFIGS, **workloads.EXTRA}[args.workload](args.seed, device=dev)
     h, hkv = w.q.shape[0], w.k.shape[0]
-    tile_q, groups, cus = _native.tile_q(h, hkv, lib), _native.head_groups(h, hkv, lib), _num_cus(dev)
+    tile_q = _native.tile_q(h, hkv, w.q.shape[2], lib=lib)
+    groups, cus = _native.head_groups(h, hkv, lib), _num_cus(dev)
 
     def host():
         TilePlan.build(w.segments, w.num_tokens, tile_q, dev).schedule(groups, cus)

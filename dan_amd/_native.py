@@ -227,7 +227,7 @@ def last_error(lib):
     return msg.decode() if msg else ""
 
 
-def tile_q(num_heads, num_kv_heads, head_dim=128, lib=None):
+def tile_q(num_heads, num_kv_heads, head_dim=128, *, lib=None):
     """Queries per work item the kernel expects (0: unsupported head layout)."""
     return (lib or load()).dan_tree_attn_tile_q(num_heads, num_kv_heads, head_dim)
 

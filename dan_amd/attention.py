@@ -322,7 +322,11 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
     call wrote there -- bench.py times the attention launch alone that way.
     ``noalloc`` launches through ``dan_tree_attn_fwd_noalloc`` (the V^T copy in
     the library's own per-GPU scratch instead of a workspace)."""
-    if phases != _native.PHASES_ALL and workspace is None and not noalloc:
+    if phases != _native.PHASES_ALL and noalloc:
+        # the operator declares no mutation of the library's scratch, so a
+        # split pack / attend pair through it could be reordered or dropped
+        raise ValueError("noalloc calls run both phases (PHASES_ALL); a split call needs a workspace")
+    if phases != _native.PHASES_ALL and workspace is None:
         raise ValueError("a split call (PHASE_PACK / PHASE_ATTEND) needs the workspace the two phases share")
     return torch.ops.dan_amd.tree_attn(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc),
                                        workspace)
@@ -517,6 +521,8 @@ class BudgetPlan:
         self.tables = {}  # layer -> (device DanPastDesc table, pinned staging)
         self.refs = []
         self.loaded = None
+        self.loaded_layers = set()   # the layers whose prefix tables the last load wrote
+        self.loaded_has_past = False  # whether the loaded batch has prefix-cache entries
         self._copied = torch.cuda.Event()
         self._copied.record(torch.cuda.current_stream(device))
 
@@ -530,7 +536,12 @@ class BudgetPlan:
     def load(self, segments, layers=None):
         """Plan ``segments`` (a Batch over this budget's tokens) on the device and
         write the prefix tables of ``layers`` (default: every layer its
-        prefix-cache entries hold, and every layer already captured)."""
+        prefix-cache entries hold, and every layer already captured).
+
+        Every check runs and every layer's table is built on the host before
+        anything is copied to the device: a batch that fails them (too large,
+        a layer its entries lack, a past length or dtype that does not match)
+        raises and leaves the previously loaded batch in place."""
         from .plan import device_inputs
 
         lib = _native.load()
@@ -540,6 +551,17 @@ class BudgetPlan:
             raise ValueError(f"batch of {len(segs)} segments, {len(starts)} branches, {w} work items, {c} V^T column "
                              f"blocks exceeds the capacities ({self.max_segments}, {self.max_branches}, "
                              f"{self.max_work}, {self.max_cols})")
+        if layers is None:
+            layers = set(self.tables)
+            if past_dicts:
+                layers |= set.intersection(*(set(pd) for pd in past_dicts))
+        built, refs = {}, []
+        for layer in sorted(layers):
+            if any(layer not in pd for pd in past_dicts):
+                raise KeyError(f"layer {layer}: a prefix-cache entry of this batch holds no such layer")
+            raw, r = _past_descs(past_dicts, segs, layer, self.hkv, self.d, self.dtype, self.device, self.max_segments)
+            built[layer] = raw
+            refs += r
         stream = torch.cuda.current_stream(self.device)
         self._copied.synchronize()  # the previous upload has left the staging buffers
         st = self.staging.numpy()
@@ -547,14 +569,7 @@ class BudgetPlan:
         st[4:4 + segs.size] = segs.ravel()
         st[4 + 8 * self.max_segments:4 + 8 * self.max_segments + len(starts)] = starts
         self.blob.copy_(self.staging, non_blocking=True)
-        if layers is None:
-            layers = set(self.tables)
-            if past_dicts:
-                layers |= set.intersection(*(set(pd) for pd in past_dicts))
-        refs = []
-        for layer in sorted(layers):
-            raw, r = _past_descs(past_dicts, segs, layer, self.hkv, self.d, self.dtype, self.device, self.max_segments)
-            refs += r
+        for layer, raw in built.items():
             table = self._table(layer)
             stage = self.tables[layer][1]
             stage.copy_(raw)
@@ -573,6 +588,8 @@ class BudgetPlan:
         self._copied.record(stream)
         self.refs = refs  # the prefix entries (and staged copies) the tables point at
         self.loaded = segments
+        self.loaded_layers = set(built)
+        self.loaded_has_past = bool(past_dicts)
 
     def attend(self, q, k, v, layer, scale=None, *, q_scale=None, k_scale=None, v_scale=None):
         """``attend(q, k, v, batch, layer)`` over the batch ``load`` uploaded, with
@@ -586,6 +603,11 @@ class BudgetPlan:
                              f"{self.dtype} with {self.hkv} kv heads")
         if self.loaded is None:
             raise ValueError("load a batch before attend")
+        if self.loaded_has_past and layer not in self.loaded_layers:
+            # the layer's prefix table was not written for this batch: the V^T
+            # copy and the attention would read prefix entries through it
+            raise KeyError(f"layer {layer}: the loaded batch has prefix-cache entries, but load() wrote no prefix "
+                           f"table for this layer (loaded: {sorted(self.loaded_layers)})")
         scales = []
         if q.dtype == E4M3:
             scales = [_check_scale(t, nm, q.device) for t, nm in

@@ -984,15 +984,20 @@ void tree_attn_kernel(const KParams args) {
     // max (O and l rescaled), so every p stays below 2^15. The check reads S
     // only, so P V does not wait on the row sum. A lane holds half of its
     // query's keys and the other half sits in lane ^ 32; both keep the same m.
-    auto lane_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the lane's 32 keys
-      float m8[8];
+    // max S over the lane's 32 keys: a tree of three-input maxima (v_max3_f32,
+    // two values per instruction): 32 -> 12 -> 4 -> 1 in 16 instructions.
+    auto lane_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {
+      auto e = [&](int i) __attribute__((always_inline)) { return s[i >> 4][i & 15]; };
+      auto max3 = [](float a, float b, float c) __attribute__((always_inline)) { return fmaxf(fmaxf(a, b), c); };
+      float m12[12];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) m8[i] = fmaxf(fmaxf(s[0][2 * i], s[0][2 * i + 1]), fmaxf(s[1][2 * i], s[1][2 * i + 1]));
+      for (int i = 0; i < 10; ++i) m12[i] = max3(e(3 * i), e(3 * i + 1), e(3 * i + 2));
+      m12[10] = e(30);
+      m12[11] = e(31);
+      float m4[4];
 #pragma unroll
-      for (int w2 = 4; w2 >= 1; w2 >>= 1)
-#pragma unroll
-        for (int i = 0; i < w2; ++i) m8[i] = fmaxf(m8[i], m8[i + w2]);
-      return m8[0];
+      for (int i = 0; i < 4; ++i) m4[i] = max3(m12[3 * i], m12[3 * i + 1], m12[3 * i + 2]);
+      return fmaxf(max3(m4[0], m4[1], m4[2]), m4[3]);
     };
     auto s_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {  // max S over the query's keys
       const LanePair mp = lane_pair(lane_max(s));

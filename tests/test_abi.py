@@ -101,18 +101,18 @@ def test_ctypes_layout_matches_header(tmp_path):
 
 def test_abi_version_and_tile_q(lib):
     assert lib.dan_tree_attn_abi_version() == _native.ABI_VERSION
-    assert _native.tile_q(32, 8, 128, lib) == 64   # rep 4: 4 heads x 64 tokens per work group
-    assert _native.tile_q(8, 2, 128, lib) == 64
-    assert _native.tile_q(14, 2, 128, lib) == 64   # rep 7: two head chunks
-    assert _native.tile_q(16, 8, 128, lib) == 128  # rep 2
-    assert _native.tile_q(8, 8, 128, lib) == 256   # rep 1
-    assert _native.tile_q(8, 8, 64, lib) == 256
-    assert _native.tile_q(16, 2, 256, lib) == 32   # head_dim 256: 4 waves, 4 heads x 32 tokens
-    assert _native.tile_q(16, 8, 256, lib) == 64
-    assert _native.tile_q(8, 8, 256, lib) == 128
-    assert _native.tile_q(8, 8, 96, lib) == 0      # head_dim not built
-    assert _native.tile_q(12, 8, 128, lib) == 0    # not a multiple
-    assert _native.tile_q(0, 8, 128, lib) == 0
+    assert _native.tile_q(32, 8, 128, lib=lib) == 64   # rep 4: 4 heads x 64 tokens per work group
+    assert _native.tile_q(8, 2, 128, lib=lib) == 64
+    assert _native.tile_q(14, 2, 128, lib=lib) == 64   # rep 7: two head chunks
+    assert _native.tile_q(16, 8, 128, lib=lib) == 128  # rep 2
+    assert _native.tile_q(8, 8, 128, lib=lib) == 256   # rep 1
+    assert _native.tile_q(8, 8, 64, lib=lib) == 256
+    assert _native.tile_q(16, 2, 256, lib=lib) == 32   # head_dim 256: 4 waves, 4 heads x 32 tokens
+    assert _native.tile_q(16, 8, 256, lib=lib) == 64
+    assert _native.tile_q(8, 8, 256, lib=lib) == 128
+    assert _native.tile_q(8, 8, 96, lib=lib) == 0      # head_dim not built
+    assert _native.tile_q(12, 8, 128, lib=lib) == 0    # not a multiple
+    assert _native.tile_q(0, 8, 128, lib=lib) == 0
     assert _native.head_groups(32, 8, lib) == 8     # rep 4: one chunk per kv head
     assert _native.head_groups(14, 2, lib) == 4     # rep 7: two chunks
     assert _native.head_groups(16, 8, lib) == 8

@@ -92,6 +92,45 @@ def test_one_graph_serves_changing_batches(gpu):
             assert same
 
 
+def test_unloaded_layer_is_refused(gpu):
+    """A batch with prefix-cache entries: attend on a layer whose prefix table
+    load() did not write is refused on the host (its table would point the
+    V^T copy at no entry), so is a load of a layer the entries lack, and the
+    loaded batch still serves its own layer afterwards."""
+    w = W.runner_shapes(0, device=gpu)
+    bp = plan_for(w, gpu)
+    bp.load(w.segments)
+    other = w.layer + 1
+    with pytest.raises(KeyError, match="prefix table"):
+        bp.attend(w.q, w.k, w.v, other)
+    with pytest.raises(KeyError, match="no such layer"):
+        bp.load(w.segments, layers=[other])
+    got = bp.attend(w.q, w.k, w.v, w.layer)
+    want = attend(w.q, w.k, w.v, w.segments, w.layer)
+    torch.cuda.synchronize()
+    rows = rows_of(w)
+    assert torch.equal(got[:, rows], want[:, rows])
+
+
+def test_failed_load_keeps_the_loaded_batch(gpu):
+    """A load whose prefix entry does not match its segment (past length)
+    raises before anything is uploaded: the batch loaded before still
+    gives its own outputs."""
+    w, w2 = W.runner_shapes(0, device=gpu), W.runner_shapes(1, device=gpu)
+    bp = plan_for(w, gpu)
+    bp.load(w.segments)
+    seg = next(s for s in w2.segments if s.past)
+    pk, pv = seg.past[w2.layer]
+    seg.past[w2.layer] = (pk[:, :-1], pv[:, :-1])
+    with pytest.raises(ValueError, match="past"):
+        bp.load(w2.segments)
+    got = bp.attend(w.q, w.k, w.v, w.layer)
+    want = attend(w.q, w.k, w.v, w.segments, w.layer)
+    torch.cuda.synchronize()
+    rows = rows_of(w)
+    assert torch.equal(got[:, rows], want[:, rows])
+
+
 def test_capacities_are_checked(gpu):
     w = W.config2(0, device=gpu)
     bp = plan_for(w, gpu, max_segments=2)

@@ -5,11 +5,15 @@ e4m3 inputs alike. This test recomputes config 5's readout rows (the last
 token of every branch; c5 = config 3 quantized to e4m3) with P rounded to
 fp16, to bf16, and to e4m3 (3 significant bits, as an fp8 P V product on the
 matrix core would need), each with the normalizer summed from the rounded
-P, against the fp32 oracle on the same dequantized inputs. Only fp16 P keeps
-the readout within 1e-3; e4m3 P misses even the fp8 readout bar of 1e-2 on
-its own (measured: fp16 7.3e-4, bf16 2.3e-3, e4m3 3.0e-2). The rounded-P
-softmax is written here for the read rows only; without rounding it equals
-the oracle's rows within 1e-5."""
+P, against the fp32 oracle on the same dequantized inputs. e4m3 P is tried
+as it is (p <= 1) and with the power-of-two scales an fp8 P V would use to
+move P up e4m3's range: P * 2^8, and P * 448 (the row's largest p at
+e4m3's largest value; 448 = 2^8 * 1.75). Only fp16 P keeps the readout
+within 1e-3; every e4m3 form misses even the fp8 readout bar of 1e-2 on its
+own (measured: fp16 7.3e-4, bf16 2.3e-3, e4m3 3.0e-2, e4m3 at P * 2^8
+3.0e-2, e4m3 at P * 448 1.4e-2). The rounded-P softmax is written here for
+the read rows only; without rounding it equals the oracle's rows within
+1e-5."""
 import math
 
 import pytest
@@ -75,10 +79,13 @@ def test_p_precision_against_the_readout_bar():
     assert (exact - ref[:, rows]).abs().max().item() < 1e-5  # the restatement matches the oracle
     dp = {name: _readout_dp(_read_rows_rounded(w, q, k, v, f), exact, w)
           for name, f in (("fp16", lambda p: p.half().float()), ("bf16", lambda p: p.bfloat16().float()),
-                          ("e4m3", lambda p: p.to(torch.float8_e4m3fn).float()))}
+                          ("e4m3", lambda p: p.to(torch.float8_e4m3fn).float()),
+                          ("e4m3 P*2^8", lambda p: (p * 256.0).to(torch.float8_e4m3fn).float()),
+                          ("e4m3 P*448", lambda p: (p * 448.0).to(torch.float8_e4m3fn).float()))}
     print(dp)
     assert dp["fp16"] <= 1e-3
-    assert dp["e4m3"] > 1e-2
+    # a scale multiplies the normalizer as well: it cancels in O / l, only the rounding differs
+    assert dp["e4m3"] > 1e-2 and dp["e4m3 P*2^8"] > 1e-2 and dp["e4m3 P*448"] > 1e-2
 
 
 def _dequant_entry(s, layer):

@@ -31,7 +31,19 @@ def test_noalloc_equals_workspace_path_two_calls(gpu):
         assert torch.isfinite(got).all()
 
 
-def test_noalloc_e4m3_and_attend_only_phase(gpu):
+def test_noalloc_e4m3(gpu):
     w = workloads.config5(0, device=gpu)
     ref, got = _both(w)
     assert torch.equal(ref, got)
+
+
+def test_noalloc_refuses_split_phases(gpu):
+    """A split (pack-only or attend-only) call would read or leave the V^T
+    copy in the shared scratch across operator calls that declare no
+    mutation; it is refused on the host before anything is launched."""
+    from dan_amd import _native
+
+    w = workloads.config1(0, device=gpu)
+    for ph in (_native.PHASE_PACK, _native.PHASE_ATTEND):
+        with pytest.raises(ValueError, match="noalloc"):
+            _attend_fused(w.q, w.k, w.v, w.segments, w.layer, None, None, phases=ph, noalloc=True)
