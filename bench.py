@@ -230,12 +230,14 @@ def _event_ms(fn, steps):
 
 def bench_fp8_linear(args):
     """One decoder layer's FP8 linears (dan_amd.quant.FP8Linear, rowwise) at
-    Llama-3-8B shapes on 8192 tokens: activation quantization (this
-    package's kernel) + hipBLASLt's fp8 GEMM per linear. One step = the four
-    linears' forwards on synthetic bf16 activations and random weights."""
+    Llama-3-8B shapes on 8192 tokens: activation quantization and the scaled
+    e4m3 GEMM per linear, both this package's kernels. One step = the four
+    linears' forwards on synthetic bf16 activations and random weights.
+    hipBLASLt's GEMM (torch._scaled_mm, dan's call) is timed on the same
+    operands for comparison (`hipblaslt_gemm_ms`)."""
     from torch import nn
 
-    from dan_amd.quant import FP8Linear, fp8_quantize
+    from dan_amd.quant import FP8Linear, fp8_gemm, fp8_quantize
 
     dev = torch.device("cuda:0")
     m = 8192
@@ -268,9 +270,11 @@ def bench_fp8_linear(args):
     # parts, timed per launch on the stream
     quant_ms = [_event_ms(lambda x=x: fp8_quantize(x), args.steps) for x in xs]
     qs = [fp8_quantize(x) for x in xs]
-    gemm_ms = [_event_ms(lambda f=f, q=q: torch._scaled_mm(q[0], f.weight.t(), scale_a=q[1], scale_b=f.weight_scale,
-                                                           out_dtype=torch.bfloat16), args.steps)
-               for f, q in zip(layers, qs)]
+    gemm_ms = [_event_ms(lambda f=f, q=q: fp8_gemm(q[0], q[1], f.weight, f.weight_scale, None, torch.bfloat16),
+                         args.steps) for f, q in zip(layers, qs)]
+    lib_ms = [_event_ms(lambda f=f, q=q: torch._scaled_mm(q[0], f.weight.t(), scale_a=q[1], scale_b=f.weight_scale,
+                                                          out_dtype=torch.bfloat16), args.steps)
+              for f, q in zip(layers, qs)]
 
     def eager_quant(x):  # dan/fused.py:85-91 as eager torch ops on this GPU
         xf = x.float()
@@ -280,6 +284,7 @@ def bench_fp8_linear(args):
     eager_ms = [_event_ms(lambda x=x: eager_quant(x), args.steps) for x in xs]
     qbytes = [m * k * 2 + m * k + m * 4 for _, _, k in LLAMA8B_LINEARS]
     gemm_tf = flops / (sum(gemm_ms) * 1e-3) / 1e12
+    lib_tf = flops / (sum(lib_ms) * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import quant as OQ
@@ -305,7 +310,11 @@ def bench_fp8_linear(args):
                    "seed": args.seed},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
                      "frac": round(gemm_tf / PEAK_TFLOPS["fp8"], 4), "traffic": None,
-                     "gemm_ms": [round(x, 4) for x in gemm_ms], "quant_ms": [round(x, 4) for x in quant_ms],
+                     "gemm_ms": [round(x, 4) for x in gemm_ms],
+                     "gemm_tflops": [round(2 * m * n * k / (t * 1e-3) / 1e12, 1)
+                                     for (_, n, k), t in zip(LLAMA8B_LINEARS, gemm_ms)],
+                     "hipblaslt_gemm_ms": [round(x, 4) for x in lib_ms], "hipblaslt_frac": round(lib_tf / PEAK_TFLOPS["fp8"], 4),
+                     "quant_ms": [round(x, 4) for x in quant_ms],
                      "quant_gbps": [round(b / (t * 1e-3) / 1e9, 1) for b, t in zip(qbytes, quant_ms)],
                      "quant_hbm_frac": round(sum(qbytes) / (sum(quant_ms) * 1e-3) / 1e9 / HBM_GBPS, 4),
                      "eager_quant_ms": [round(x, 4) for x in eager_ms]},

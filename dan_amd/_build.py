@@ -8,7 +8,9 @@ Flags:
                                    ships its own HIP runtime).
   -target-feature -packed-fp32-ops no packed fp32 VALU instructions.
   -amdgpu-mfma-vgpr-form           matrix-core results in VGPRs, so the softmax
-                                   reads the score tile without AGPR copies.
+                                   reads the score tile without AGPR copies
+                                   (every source but fp8_gemm.hip, whose
+                                   accumulators fill the AGPRs).
   -fno-honor-nans -mno-amdgpu-ieee tree_attn.hip only: v_max_f32 without a
                                    canonicalizing max in front of every operand
                                    (the attention's running-max raise). The
@@ -25,9 +27,14 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "gdn.hip", "gdn_chunk.hip", "gdn_conv.hip")]
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("tree_attn.hip", "qkv_front.hip", "tree_plan.hip", "fp8_quant.hip", "fp8_gemm.hip",
+                                                 "gdn.hip", "gdn_chunk.hip", "gdn_conv.hip")]
 # Extra flags per source (file name -> flags).
 SRC_FLAGS = {"tree_attn.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+# Matrix-core results in VGPRs, for every source but the GEMM, whose 256
+# accumulators per lane live in the accumulation registers (AGPRs).
+MFMA_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+ACC_IN_AGPRS = {"fp8_gemm.hip"}
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libdan_tree_attn.so")
@@ -36,7 +43,6 @@ HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 
@@ -69,8 +75,11 @@ def build(out=OUT, extra=(), verbose=False):
     obj_dir = os.path.join(os.path.dirname(out), "_obj")
     os.makedirs(obj_dir, exist_ok=True)
     objs = [os.path.join(obj_dir, os.path.basename(src) + ".o") for src in SRCS]
-    cmds = [[hipcc(), *HIPCC_FLAGS, *SRC_FLAGS.get(os.path.basename(src), []), *extra, "-I", INCLUDE, "-c", src, "-o", obj]
-            for src, obj in zip(SRCS, objs)]
+    def flags(src):
+        name = os.path.basename(src)
+        return [*HIPCC_FLAGS, *([] if name in ACC_IN_AGPRS else MFMA_VGPR_FORM), *SRC_FLAGS.get(name, [])]
+
+    cmds = [[hipcc(), *flags(src), *extra, "-I", INCLUDE, "-c", src, "-o", obj] for src, obj in zip(SRCS, objs)]
     with ThreadPoolExecutor(max_workers=min(len(cmds), max(1, (os.cpu_count() or 1)))) as pool:
         for f in [pool.submit(_run, c, verbose) for c in cmds]:
             f.result()

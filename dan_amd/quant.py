@@ -4,11 +4,11 @@
 weights quantized once, per output row (rowwise) or per tensor, activations
 quantized on every call with ``scale = max(amax, 1e-12) / 448`` and
 ``xq = e4m3fn(x / scale)`` (dan/fused.py:85-91), then one scaled fp8 GEMM with
-the bias in its epilogue. The quantizer is this package's gfx950 kernel
-(``dan_fp8_quantize``, include/dan_fp8.h): one read of x per call, where
-dan's eager chain makes five passes. The GEMM is the library fp8 GEMM dan
-calls, ``torch._scaled_mm`` (dan/quant.py:40), which is hipBLASLt on gfx950
-(row and column scale vectors applied in its epilogue).
+the bias in its epilogue. Both are this package's gfx950 kernels
+(include/dan_fp8.h): the quantizer (``dan_fp8_quantize``, one read of x per
+call, where dan's eager chain makes five passes) and the scaled GEMM
+(``dan_fp8_gemm``, e4m3 x e4m3 on the matrix core with fp32 accumulation),
+which takes the place of dan's ``torch._scaled_mm`` call (dan/quant.py:39-41).
 
 There is no CPU path: CPU tensors raise (the eager CPU chain is the test
 oracle, oracle/quant.py).
@@ -53,6 +53,63 @@ def fp8_quantize(x, fp8_max=E4M3_MAX, rowwise=True):
     return xq, scale
 
 
+def fp8_gemm(xq, scale_a, wq, scale_b, bias=None, out_dtype=torch.bfloat16):
+    """``torch._scaled_mm(xq, wq.t(), scale_a, scale_b, bias, out_dtype)`` as
+    dan calls it (dan/quant.py:39-41) on gfx950: y [M, N] = (xq [M, K] wq
+    [N, K]^T) * scale_a * scale_b + bias, fp32 accumulation, rounded to
+    out_dtype. scale_a is [M, 1] or [1, 1], scale_b [1, N] or [1, 1] (fp32);
+    bias [N] of out_dtype or None. N and K are multiples of 16."""
+    if not (xq.is_cuda and wq.is_cuda):
+        raise RuntimeError("dan_amd.quant.fp8_gemm runs on a gfx950 GPU only; got tensors on "
+                           f"{xq.device} / {wq.device}")
+    if xq.dtype != E4M3 or wq.dtype != E4M3:
+        raise ValueError(f"operands must be float8_e4m3fn; got {xq.dtype} and {wq.dtype}")
+    if xq.dim() != 2 or wq.dim() != 2 or xq.shape[1] != wq.shape[1]:
+        raise ValueError(f"xq [M, K] and wq [N, K]; got {tuple(xq.shape)} and {tuple(wq.shape)}")
+    if out_dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError(f"out_dtype {out_dtype}: bf16, fp16 or fp32")
+    m, k = xq.shape
+    n = wq.shape[0]
+    flags = 0
+    if scale_a.numel() == 1 and m != 1:
+        flags |= _native.FP8_GEMM_X_SCALE_TENSOR
+    elif scale_a.numel() != m:
+        raise ValueError(f"scale_a has {scale_a.numel()} values for {m} rows")
+    if scale_b.numel() == 1 and n != 1:
+        flags |= _native.FP8_GEMM_W_SCALE_TENSOR
+    elif scale_b.numel() != n:
+        raise ValueError(f"scale_b has {scale_b.numel()} values for {n} rows")
+
+    def dense(t, dtype, name):
+        if t.dtype != dtype:
+            raise ValueError(f"{name} must be {dtype}; got {t.dtype}")
+        return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous().clone()
+
+    sa, sb = dense(scale_a, torch.float32, "scale_a"), dense(scale_b, torch.float32, "scale_b")
+    if bias is not None:
+        bias = dense(bias, out_dtype, "bias")
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} values for {n} outputs")
+
+    def rows(t):  # 16-byte aligned rows of unit column stride
+        if t.stride(1) != 1 or t.stride(0) % 16 or t.data_ptr() % 16 or t.stride(0) < t.shape[1]:
+            return t.contiguous().clone()
+        return t
+
+    xq, wq = rows(xq), rows(wq)
+    y = torch.empty((m, n), dtype=out_dtype, device=xq.device)
+    a = _native.DanFp8GemmArgs()
+    a.abi_version = _native.FP8_ABI_VERSION
+    a.out_dtype = _DTYPES[out_dtype]
+    a.m, a.n, a.k, a.flags = m, n, k, flags
+    a.xq, a.xq_stride, a.x_scale = xq.data_ptr(), xq.stride(0), sa.data_ptr()
+    a.wq, a.wq_stride, a.w_scale = wq.data_ptr(), wq.stride(0), sb.data_ptr()
+    a.bias = bias.data_ptr() if bias is not None else None
+    a.y, a.y_stride = y.data_ptr(), y.stride(0)
+    _native.fp8_gemm(a, torch.cuda.current_stream(xq.device).cuda_stream)
+    return y
+
+
 def supported(device=None):
     """gfx950 (OCP e4m3 matrix cores)."""
     if not torch.cuda.is_available():
@@ -78,8 +135,7 @@ class FP8Linear(nn.Module):
     def forward(self, x):
         shape = x.shape
         xq, scale = fp8_quantize(x.reshape(-1, shape[-1]), E4M3_MAX, self.rowwise)
-        y = torch._scaled_mm(xq, self.weight.t(), scale_a=scale, scale_b=self.weight_scale,
-                             bias=self.bias, out_dtype=self.out_dtype)
+        y = fp8_gemm(xq, scale, self.weight, self.weight_scale, self.bias, self.out_dtype)
         return y.reshape(*shape[:-1], self.out_features)
 
 

@@ -1,6 +1,6 @@
 /*
- * dan_fp8.h -- C ABI of the gfx950 e4m3 quantizer for dan's FP8 decoder
- * linears.
+ * dan_fp8.h -- C ABI of the gfx950 e4m3 quantizer and e4m3 GEMM for dan's
+ * FP8 decoder linears.
  *
  * dan's FP8Linear (dan/quant.py:23-42) quantizes its weight once (per output
  * row, or per tensor) and its input on every call with fp8_quantize
@@ -9,10 +9,10 @@
  *     scale = max(amax, 1e-12) / 448            (fp32)
  *     xq    = e4m3fn(x / scale)                  (fp32 divide, round to nearest even)
  * and then multiplies with torch._scaled_mm (dan/quant.py:40), a library fp8
- * GEMM with the two scale vectors and the bias in its epilogue. On gfx950 that
- * GEMM is hipBLASLt's (OCP e4m3, v_mfma_*_f8f6f4); this library supplies the
- * quantizer: one read of x and one write of xq per call (rowwise), where the
- * eager chain makes five passes.
+ * GEMM with the two scale vectors and the bias in its epilogue. This library
+ * supplies both halves: the quantizer (one read of x and one write of xq per
+ * call, rowwise, where the eager chain makes five passes) and the scaled GEMM
+ * (v_mfma_f32_32x32x64_f8f6f4, OCP e4m3, fp32 accumulation).
  *
  * Conventions are those of dan_tree_attn.h: caller-owned device memory,
  * nothing allocated or kept, asynchronous on `stream`, 0 on success and a
@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DAN_FP8_ABI_VERSION 1
+#define DAN_FP8_ABI_VERSION 2
 
 typedef enum {
   DAN_FP8_SCALE_TENSOR = 0, /* one scale for the whole tensor (dan's sm89 mode) */
@@ -52,6 +52,34 @@ typedef struct {
 /* Quantize x to e4m3fn with dan's scale convention.
  * Replaces dan/fused.py:85-91 (fp8_quantize) on gfx950. */
 int dan_fp8_quantize(const DanFp8QuantArgs *args, void *stream);
+
+/* Flags of DanFp8GemmArgs: a scale given per tensor (one value) instead of per row. */
+#define DAN_FP8_GEMM_X_SCALE_TENSOR 1
+#define DAN_FP8_GEMM_W_SCALE_TENSOR 2
+
+typedef struct {
+  int32_t abi_version;  /* DAN_FP8_ABI_VERSION */
+  int32_t out_dtype;    /* DanDtype of y and bias: bf16, f16 or f32 */
+  int32_t m;            /* rows of xq and y (tokens) */
+  int32_t n;            /* rows of wq, columns of y (output features): a multiple of 16 */
+  int32_t k;            /* columns of xq and wq (input features): a multiple of 16 */
+  int32_t flags;        /* DAN_FP8_GEMM_* */
+  const uint8_t *xq;    /* [M, K] e4m3fn codes, row stride xq_stride bytes (16-byte aligned rows) */
+  int64_t xq_stride;
+  const float *x_scale; /* [M] fp32, or [1] with DAN_FP8_GEMM_X_SCALE_TENSOR */
+  const uint8_t *wq;    /* [N, K] e4m3fn codes (the weight as stored, not transposed) */
+  int64_t wq_stride;
+  const float *w_scale; /* [N] fp32 (16-byte aligned), or [1] with DAN_FP8_GEMM_W_SCALE_TENSOR */
+  const void *bias;     /* [N] of out_dtype (16-byte aligned), or NULL */
+  void *y;              /* [M, N] of out_dtype, row stride y_stride elements (16-byte aligned rows) */
+  int64_t y_stride;
+} DanFp8GemmArgs;
+
+/* y = (xq wq^T) * x_scale[m] * w_scale[n] + bias[n], fp32 accumulation, rounded
+ * to out_dtype (to nearest even).
+ * Replaces dan/quant.py:39-41 (torch._scaled_mm(xq, weight.t(), scale_a,
+ * scale_b, bias, out_dtype) in FP8Linear.forward) on gfx950. */
+int dan_fp8_gemm(const DanFp8GemmArgs *args, void *stream);
 
 int dan_fp8_abi_version(void);
 
