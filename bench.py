@@ -233,8 +233,9 @@ def bench_fp8_linear(args):
     Llama-3-8B shapes on 8192 tokens: activation quantization and the scaled
     e4m3 GEMM per linear, both this package's kernels. One step = the four
     linears' forwards on synthetic bf16 activations and random weights.
-    hipBLASLt's GEMM (torch._scaled_mm, dan's call) is timed on the same
-    operands for comparison (`hipblaslt_gemm_ms`)."""
+    The GEMM is timed on the tiled operands FP8Linear hands it (`gemm_ms`),
+    on row-major operands (`rows_gemm_ms`), and hipBLASLt's GEMM
+    (torch._scaled_mm, dan's call) on the same codes (`hipblaslt_gemm_ms`)."""
     from torch import nn
 
     from dan_amd.quant import FP8Linear, fp8_gemm, fp8_quantize
@@ -268,10 +269,15 @@ def bench_fp8_linear(args):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t) / args.steps
     # parts, timed per launch on the stream
-    quant_ms = [_event_ms(lambda x=x: fp8_quantize(x), args.steps) for x in xs]
-    qs = [fp8_quantize(x) for x in xs]
-    gemm_ms = [_event_ms(lambda f=f, q=q: fp8_gemm(q[0], q[1], f.weight, f.weight_scale, None, torch.bfloat16),
+    quant_ms = [_event_ms(lambda x=x: fp8_quantize(x, tiled=True), args.steps) for x in xs]
+    qs = [fp8_quantize(x) for x in xs]  # row-major codes (hipBLASLt's and the row-major GEMM's operand)
+    qt = [fp8_quantize(x, tiled=True) for x in xs]
+    gemm_ms = [_event_ms(lambda f=f, q=q: fp8_gemm(q[0], q[1], f.tiled_weight(), f.weight_scale, None, torch.bfloat16),
+                         args.steps) for f, q in zip(layers, qt)]
+    rows_ms = [_event_ms(lambda f=f, q=q: fp8_gemm(q[0], q[1], f.weight, f.weight_scale, None, torch.bfloat16),
                          args.steps) for f, q in zip(layers, qs)]
+    for f, q in zip(layers, qs):  # hipBLASLt picks its kernel on a shape's first call
+        torch._scaled_mm(q[0], f.weight.t(), scale_a=q[1], scale_b=f.weight_scale, out_dtype=torch.bfloat16)
     lib_ms = [_event_ms(lambda f=f, q=q: torch._scaled_mm(q[0], f.weight.t(), scale_a=q[1], scale_b=f.weight_scale,
                                                           out_dtype=torch.bfloat16), args.steps)
               for f, q in zip(layers, qs)]
@@ -313,6 +319,7 @@ def bench_fp8_linear(args):
                      "gemm_ms": [round(x, 4) for x in gemm_ms],
                      "gemm_tflops": [round(2 * m * n * k / (t * 1e-3) / 1e12, 1)
                                      for (_, n, k), t in zip(LLAMA8B_LINEARS, gemm_ms)],
+                     "rows_gemm_ms": [round(x, 4) for x in rows_ms],
                      "hipblaslt_gemm_ms": [round(x, 4) for x in lib_ms], "hipblaslt_frac": round(lib_tf / PEAK_TFLOPS["fp8"], 4),
                      "quant_ms": [round(x, 4) for x in quant_ms],
                      "quant_gbps": [round(b / (t * 1e-3) / 1e9, 1) for b, t in zip(qbytes, quant_ms)],

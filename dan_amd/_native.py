@@ -119,12 +119,13 @@ class DanTreePlanArgs(ctypes.Structure):
 
 FP8_ABI_VERSION = 2
 FP8_SCALE_TENSOR, FP8_SCALE_ROW = 0, 1
-FP8_GEMM_X_SCALE_TENSOR, FP8_GEMM_W_SCALE_TENSOR = 1, 2
+FP8_GEMM_X_SCALE_TENSOR, FP8_GEMM_W_SCALE_TENSOR, FP8_GEMM_X_TILED, FP8_GEMM_W_TILED = 1, 2, 4, 8
+FP8_LAYOUT_ROWS, FP8_LAYOUT_TILED = 0, 1
 
 
 class DanFp8QuantArgs(ctypes.Structure):
     _fields_ = [("abi_version", _i32), ("dtype", _i32), ("rows", _i32), ("cols", _i32), ("mode", _i32),
-                ("reserved", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
+                ("layout", _i32), ("x", _vp), ("x_stride", _i64), ("xq", _vp), ("scale", _vp)]
 
 
 class DanFp8GemmArgs(ctypes.Structure):
@@ -161,7 +162,7 @@ class DanGdnConvArgs(ctypes.Structure):
 EXPORTS = ("dan_tree_attn_fwd", "dan_tree_attn_fwd_noalloc", "dan_tree_attn_stage_f16", "dan_tree_attn_tile_q", "dan_tree_attn_head_groups", "dan_tree_attn_workspace_size",
            "dan_tree_attn_last_error", "dan_tree_attn_abi_version", "dan_qkv_front", "dan_qkv_front_abi_version",
            "dan_tree_attn_plan", "dan_tree_attn_plan_slots", "dan_tree_attn_plan_abi_version",
-           "dan_fp8_quantize", "dan_fp8_gemm", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version",
+           "dan_fp8_quantize", "dan_fp8_gemm", "dan_fp8_tiled_bytes", "dan_fp8_abi_version", "dan_gdn_fwd", "dan_gdn_workspace_size", "dan_gdn_abi_version",
            "dan_gdn_conv")
 
 _lock = threading.Lock()
@@ -210,6 +211,8 @@ def load(path=LIB_PATH):
         lib.dan_fp8_quantize.restype = ctypes.c_int
         lib.dan_fp8_gemm.argtypes = [ctypes.POINTER(DanFp8GemmArgs), _vp]
         lib.dan_fp8_gemm.restype = ctypes.c_int
+        lib.dan_fp8_tiled_bytes.argtypes = [_i32, _i32]
+        lib.dan_fp8_tiled_bytes.restype = _i64
         lib.dan_fp8_abi_version.argtypes = []
         lib.dan_fp8_abi_version.restype = ctypes.c_int
         lib.dan_gdn_fwd.argtypes = [ctypes.POINTER(DanGdnArgs), _vp]
@@ -303,6 +306,11 @@ def fp8_quantize(args, stream, lib=None):
     rc = lib.dan_fp8_quantize(ctypes.byref(args), _vp(stream))
     if rc != OK:
         raise RuntimeError(f"dan_fp8_quantize failed ({rc}): {last_error(lib)}")
+
+
+def fp8_tiled_bytes(rows, cols, lib=None):
+    """Bytes of an [rows, cols] e4m3 tensor in the GEMM's tiled layout."""
+    return (lib or load()).dan_fp8_tiled_bytes(rows, cols)
 
 
 def fp8_gemm(args, stream, lib=None):

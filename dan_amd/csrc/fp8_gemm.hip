@@ -102,6 +102,7 @@ struct Params {
   int64_t y_st;            // row stride in elements
   int32_t m, n, k;
   int32_t tiles_m, tiles_n;
+  int32_t x_tiled, w_tiled;  // operand in the tiled layout (include/dan_fp8.h)
 };
 
 __device__ inline uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -118,6 +119,24 @@ __device__ inline i32x4 resource(const void *base, uint32_t bytes) {
   r[2] = (int32_t)uniform(bytes);
   r[3] = 0x00020000;
   return r;
+}
+
+// Where a wave's direct loads read: a tile's operand panel as a buffer
+// resource, each load's per-lane offset, and the offset step per k-step.
+// Rows: the panel's valid rows at their stride; a k-step is 64 bytes further.
+// Tiled: the panel's run of 16 KB k-steps; load i of the wave reads block
+// (row block) b, 16 bytes per lane, already in LDS order.
+struct Panel {
+  i32x4 rsrc;
+  uint32_t kstep;  // offset of the next k-step
+};
+__device__ inline Panel panel_of(const Params &p, bool w, int row0, int kt) {
+  const bool tiled = w ? p.w_tiled : p.x_tiled;
+  const uint8_t *ptr = w ? p.w : p.x;
+  if (tiled) return Panel{resource(ptr + (int64_t)(row0 / kTile) * kt * 16384, (uint32_t)kt * 16384u), 16384u};
+  const int64_t st = w ? p.w_st : p.x_st;
+  const int rows = min(kTile, (w ? p.n : p.m) - row0);
+  return Panel{resource(ptr + (int64_t)row0 * st, (uint32_t)(rows * st)), (uint32_t)kBK};
 }
 
 #pragma clang diagnostic push
@@ -232,15 +251,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // Load i of wave v moves 16 rows (1 KB): block b = 8 v + i of the stage; lane
   // l writes row 16 (b % 16) + l / 4 at position l % 4, holding chunk (l % 4) ^ f(row).
   const bool loads_w = wave < 2;
+  const bool tiled = loads_w ? p.w_tiled : p.x_tiled;
   const int64_t st = loads_w ? p.w_st : p.x_st;
-  const int rows = loads_w ? min(kTile, p.n - n0) : min(kTile, p.m - m0);
-  const uint8_t *base = loads_w ? p.w + (int64_t)n0 * p.w_st : p.x + (int64_t)m0 * p.x_st;
-  i32x4 rsrc = resource(base, (uint32_t)(rows * st));
+  const Panel pan = panel_of(p, loads_w, loads_w ? n0 : m0, (p.k + kBK - 1) / kBK);
+  const i32x4 rsrc = pan.rsrc;
   const int rl = lane >> 2;
   const int chunk = (lane & 3) ^ swz(rl);
   uint32_t voff[kLoadsPerWave];
 #pragma unroll
-  for (int i = 0; i < kLoadsPerWave; ++i) voff[i] = (uint32_t)((16 * ((wave * kLoadsPerWave + i) & 15) + rl) * st + 16 * chunk);
+  for (int i = 0; i < kLoadsPerWave; ++i) {
+    const int blk = (wave * kLoadsPerWave + i) & 15;
+    voff[i] = tiled ? (uint32_t)(blk * 1024 + 16 * lane) : (uint32_t)((16 * blk + rl) * st + 16 * chunk);
+  }
   const uint32_t lds_load = lds_base + wave * kLoadsPerWave * 1024;
 
   const int kt = (p.k + kBK - 1) / kBK;
@@ -248,14 +270,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // resource base by 64 bytes per step keeps the per-lane offsets fixed; the
   // shortened resource still ends at the last valid row's end.
   auto issue = [&](int s) __attribute__((always_inline)) {
-    const uint32_t k0 = (uint32_t)s * kBK;
+    const uint32_t k0 = (uint32_t)s * kBK, adv = (uint32_t)s * pan.kstep;
     i32x4 r = rsrc;
-    const uint64_t b = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + k0;
+    const uint64_t b = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + adv;
     r[0] = (int32_t)(uint32_t)b;
     r[1] = (int32_t)((uint32_t)(b >> 32) & 0xffff);
-    r[2] = (int32_t)((uint32_t)r[2] - k0);
+    r[2] = (int32_t)((uint32_t)r[2] - adv);
     const uint32_t lds = lds_load + (s & (kStages - 1)) * kStageBytes;
-    const bool full = !kTail || (int)k0 + kBK <= p.k;
+    const bool full = !kTail || tiled || (int)k0 + kBK <= p.k;  // tiled padding holds zeros
 #pragma unroll
     for (int i = 0; i < kLoadsPerWave; ++i) {
       uint32_t off = voff[i];
@@ -287,14 +309,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // a fragment read and/or a direct load as kReadSlots and kLoadSlots place them.
   auto step = [&](int s, Frags &cur, Frags &nxt, bool do_read, bool do_issue) __attribute__((always_inline)) {
     const uint32_t stage = (uint32_t)((s + 1) & (kStages - 1)) * kStageBytes;
-    const uint32_t k0 = (uint32_t)(s + 4) * kBK;
+    const uint32_t k0 = (uint32_t)(s + 4) * kBK, adv = (uint32_t)(s + 4) * pan.kstep;
     i32x4 r = rsrc;
-    const uint64_t b64 = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + k0;
+    const uint64_t b64 = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + adv;
     r[0] = (int32_t)(uint32_t)b64;
     r[1] = (int32_t)((uint32_t)(b64 >> 32) & 0xffff);
-    r[2] = (int32_t)((uint32_t)r[2] - k0);
+    r[2] = (int32_t)((uint32_t)r[2] - adv);
     const uint32_t lds = lds_load + (s & (kStages - 1)) * kStageBytes;
-    const bool full = !kTail || (int)k0 + kBK <= p.k;
+    const bool full = !kTail || tiled || (int)k0 + kBK <= p.k;
 #pragma unroll
     for (int slot = 0; slot < 16; ++slot) {
       const int a = slot >> 2, bb = slot & 3;
@@ -515,31 +537,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
   // direct-load geometry (as in fp8_gemm_kernel)
   const bool loads_w = wave < 2;
+  const bool tiled = loads_w ? p.w_tiled : p.x_tiled;
   const int64_t st = loads_w ? p.w_st : p.x_st;
   const int rl = lane >> 2;
   const int chunk = (lane & 3) ^ swz(rl);
-  // load i's offset: vbase + (row block (wave % 2) * 8 + i) * 16 rows; only
-  // the per-lane base stays in a register over the loop
-  const uint32_t vbase = (uint32_t)(rl * st + 16 * chunk);
-  const uint32_t rows16 = uniform((uint32_t)(16 * st)), wrows = uniform((uint32_t)((wave & 1) * 128 * st));
+  // load i's offset: vbase + (row block (wave % 2) * 8 + i) * (16 rows or one
+  // 1 KB tiled block); only the per-lane base stays in a register over the loop
+  const uint32_t vbase = tiled ? (uint32_t)(16 * lane) : (uint32_t)(rl * st + 16 * chunk);
+  const uint32_t blk_step = uniform(tiled ? 1024u : (uint32_t)(16 * st));
+  const uint32_t rows16 = blk_step, wrows = uniform((uint32_t)(wave & 1) * 8 * blk_step);
   const uint32_t lds_load = lds_base + wave * kLoadsPerWave * 1024;
   const int kt = (p.k + kBK - 1) / kBK;
+  const uint32_t kstep = tiled ? 16384u : (uint32_t)kBK;
   auto operand_rsrc = [&](int j) __attribute__((always_inline)) {
     if (j >= my_tiles) return resource(p.x, 0);  // past the last tile: every read out of range
     const PTile tl = tile_at(j);
-    const int rows = loads_w ? min(kTile, p.n - tl.n0) : min(kTile, p.m - tl.m0);
-    const uint8_t *base = loads_w ? p.w + (int64_t)tl.n0 * p.w_st : p.x + (int64_t)tl.m0 * p.x_st;
-    return resource(base, (uint32_t)(rows * st));
+    return panel_of(p, loads_w, loads_w ? tl.n0 : tl.m0, kt).rsrc;
   };
   // the direct loads of step s of tile j (tile j past the last: zeros)
   auto issue = [&](i32x4 rsrc, int s, uint32_t lds, bool ok) __attribute__((always_inline)) {
-    const uint32_t k0 = (uint32_t)s * kBK;
+    const uint32_t k0 = (uint32_t)s * kBK, adv = (uint32_t)s * kstep;
     i32x4 r = rsrc;
-    const uint64_t bb = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + k0;
+    const uint64_t bb = ((uint64_t)(uint32_t)r[0] | ((uint64_t)(uint32_t)(r[1] & 0xffff) << 32)) + adv;
     r[0] = (int32_t)(uint32_t)bb;
     r[1] = (int32_t)((uint32_t)(bb >> 32) & 0xffff);
-    r[2] = ok ? (int32_t)((uint32_t)r[2] - k0) : 0;
-    const bool full = !kTail || (int)k0 + kBK <= p.k;
+    r[2] = ok ? (int32_t)((uint32_t)r[2] - adv) : 0;
+    const bool full = !kTail || tiled || (int)k0 + kBK <= p.k;  // tiled padding holds zeros
     return [=](int i) __attribute__((always_inline)) {
       uint32_t off = vbase + (wrows + i * rows16);
       if (kTail && !full && (int)k0 + 16 * chunk >= p.k) off = kOutOfRange;
@@ -783,23 +806,29 @@ int dan_fp8_gemm(const DanFp8GemmArgs *a, void *stream) {
   if (a->m < 0 || a->n < 0 || a->k < 0) return fail(DAN_ERR_INVALID_ARGUMENT, "negative shape");
   if (a->k % 16 || a->n % 16)
     return fail(DAN_ERR_INVALID_ARGUMENT, "k %d and n %d must be multiples of 16", a->k, a->n);
-  if (a->flags & ~(DAN_FP8_GEMM_X_SCALE_TENSOR | DAN_FP8_GEMM_W_SCALE_TENSOR))
+  if (a->flags & ~(DAN_FP8_GEMM_X_SCALE_TENSOR | DAN_FP8_GEMM_W_SCALE_TENSOR | DAN_FP8_GEMM_X_TILED | DAN_FP8_GEMM_W_TILED))
     return fail(DAN_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", a->flags);
   if (a->m == 0 || a->n == 0) return DAN_OK;
   if (!a->xq || !a->wq || !a->x_scale || !a->w_scale || !a->y) return fail(DAN_ERR_INVALID_ARGUMENT, "NULL pointer");
   const int es = a->out_dtype == DAN_DTYPE_F32 ? 4 : 2;
-  if (((uintptr_t)a->xq & 15) || ((uintptr_t)a->wq & 15) || a->xq_stride % 16 || a->wq_stride % 16 ||
-      a->xq_stride < a->k || a->wq_stride < a->k)
-    return fail(DAN_ERR_INVALID_ARGUMENT, "xq and wq rows must be 16-byte aligned, with strides >= k");
-  if ((int64_t)256 * a->xq_stride >= ((int64_t)1 << 31) || (int64_t)256 * a->wq_stride >= ((int64_t)1 << 31))
-    return fail(DAN_ERR_UNSUPPORTED, "row strides of %lld / %lld bytes: 256 rows must span less than 2 GiB",
-                (long long)a->xq_stride, (long long)a->wq_stride);
+  const bool xt = a->flags & DAN_FP8_GEMM_X_TILED, wt = a->flags & DAN_FP8_GEMM_W_TILED;
+  if (((uintptr_t)a->xq & 15) || ((uintptr_t)a->wq & 15))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "xq and wq must be 16-byte aligned");
+  if ((!xt && (a->xq_stride % 16 || a->xq_stride < a->k)) || (!wt && (a->wq_stride % 16 || a->wq_stride < a->k)))
+    return fail(DAN_ERR_INVALID_ARGUMENT, "row-major xq and wq need strides >= k, multiples of 16 bytes");
+  // a panel (256 rows) must span less than 2 GiB: its buffer resource counts bytes in 31 bits
+  const int64_t span = (int64_t)256 * ((a->k + 63) / 64 * 64);
+  if ((xt ? span : (int64_t)256 * a->xq_stride) >= ((int64_t)1 << 31) ||
+      (wt ? span : (int64_t)256 * a->wq_stride) >= ((int64_t)1 << 31))
+    return fail(DAN_ERR_UNSUPPORTED, "256 rows of xq or wq span 2 GiB or more");
   if (((uintptr_t)a->y & 15) || (a->y_stride * es) % 16 || a->y_stride < a->n)
     return fail(DAN_ERR_INVALID_ARGUMENT, "y rows must be 16-byte aligned, with y_stride >= n");
   if (((uintptr_t)a->x_scale & 3) || ((uintptr_t)a->w_scale & 15) || ((uintptr_t)a->bias & 15))
     return fail(DAN_ERR_INVALID_ARGUMENT, "x_scale 4-byte, w_scale and bias 16-byte aligned");
   dan_gemm::Params p;
   p.x = a->xq; p.w = a->wq; p.x_st = a->xq_stride; p.w_st = a->wq_stride;
+  p.x_tiled = (a->flags & DAN_FP8_GEMM_X_TILED) != 0;
+  p.w_tiled = (a->flags & DAN_FP8_GEMM_W_TILED) != 0;
   p.xs = a->x_scale; p.ws = a->w_scale;
   p.xs_inc = (a->flags & DAN_FP8_GEMM_X_SCALE_TENSOR) ? 0 : 1;
   p.ws_inc = (a->flags & DAN_FP8_GEMM_W_SCALE_TENSOR) ? 0 : 1;

@@ -94,38 +94,72 @@ __device__ inline float scale_of(uint32_t amax_bits) {
   return amax_bits > 0x7f800000u ? amax : fmaxf(amax, 1e-12f) / kE4m3Max;
 }
 
-template <typename T>
-__device__ inline void quantize_row(const T *row, uint8_t *out, int cols, float scale) {
-  for (int c = 8 * threadIdx.x; c < cols; c += 8 * kThreads) {
-    const f32x8 x = load8<T>(row + c);
-    u32x2 q;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h] / scale, x[4 * h + 1] / scale, 0, false);
-      w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h + 2] / scale, x[4 * h + 3] / scale, w, true);
-      q[h] = (uint32_t)w;
-    }
-    *(DAN_GLOBAL u32x2 *)(out + c) = q;
-  }
-}
-
 struct Params {
   const void *x;
   int64_t x_stride;
   uint8_t *xq;
   float *scale;
   int32_t rows, cols;
+  int32_t tiled;  // DAN_FP8_LAYOUT_TILED: codes in the GEMM's panel layout
+  int32_t kt;     // 64-byte k-steps per row (tiled)
 };
+
+// Byte offset of the 8 codes of row r, columns c .. c + 7 (c a multiple of 8).
+// Tiled: 256-row panels, each a run of 16 KB k-steps; a k-step is 16 blocks
+// of 16 rows x 64 bytes, row i of a block at 64 i, its 16-byte chunk j at
+// position j ^ (((i >> 1) & 3) ^ ((i >> 3) & 1)) (include/dan_fp8.h).
+__device__ inline int64_t code_offset(const Params &p, int r, int c) {
+  if (!p.tiled) return (int64_t)r * p.cols + c;
+  const int i = r & 15, chunk = (c >> 4) & 3;
+  const int pos = chunk ^ (((i >> 1) & 3) ^ ((i >> 3) & 1));
+  return ((((int64_t)(r >> 8) * p.kt + (c >> 6)) * 16 + ((r >> 4) & 15)) << 10) + 64 * i + 16 * pos + (c & 8);
+}
+
+template <typename T>
+__device__ inline u32x2 codes8(f32x8 x, float scale) {
+  u32x2 q;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h] / scale, x[4 * h + 1] / scale, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h + 2] / scale, x[4 * h + 3] / scale, w, true);
+    q[h] = (uint32_t)w;
+  }
+  return q;
+}
+
+template <typename T>
+__device__ inline void quantize_row(const Params &p, const T *row, int r, float scale) {
+  for (int c = 8 * threadIdx.x; c < p.cols; c += 8 * kThreads)
+    *(DAN_GLOBAL u32x2 *)(p.xq + code_offset(p, r, c)) = codes8<T>(load8<T>(row + c), scale);
+}
+
+// Tiled: zeros past the row's last column, up to its last k-step's end.
+__device__ inline void zero_row_tail(const Params &p, int r) {
+  if (!p.tiled) return;
+  for (int c = p.cols + 8 * threadIdx.x; c < 64 * p.kt; c += 8 * kThreads)
+    *(DAN_GLOBAL u32x2 *)(p.xq + code_offset(p, r, c)) = (u32x2){0u, 0u};
+}
+
+// Tiled: the padding rows of the last panel are zeros. Returns true for such
+// a row (the whole work group).
+__device__ inline bool pad_row(const Params &p, int r) {
+  if (r < p.rows) return false;
+  for (int c = 8 * threadIdx.x; c < 64 * p.kt; c += 8 * kThreads)
+    *(DAN_GLOBAL u32x2 *)(p.xq + code_offset(p, r, c)) = (u32x2){0u, 0u};
+  return true;
+}
 
 // Rowwise: the row's scale, then its codes.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(const Params p) {
   __shared__ uint32_t red[4];
   const int r = blockIdx.x;
+  if (pad_row(p, r)) return;
   const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
   const float s = scale_of(block_amax(row_amax<T>(row, p.cols), red));
   if (threadIdx.x == 0) *(DAN_GLOBAL float *)(p.scale + r) = s;
-  quantize_row<T>(row, p.xq + (int64_t)r * p.cols, p.cols, s);
+  quantize_row<T>(p, row, r, s);
+  zero_row_tail(p, r);
 }
 
 // Rowwise, for rows of at most NC * 8 * kThreads values: the row stays in
@@ -136,6 +170,7 @@ template <typename T, int NC>
 __global__ __launch_bounds__(kThreads) void quant_rows_reg_kernel(const Params p) {
   __shared__ uint32_t red[4];
   const int r = blockIdx.x;
+  if (pad_row(p, r)) return;
   const T *row = static_cast<const T *>(p.x) + (int64_t)r * p.x_stride;
   f32x8 x[NC];
 #pragma unroll
@@ -149,21 +184,12 @@ __global__ __launch_bounds__(kThreads) void quant_rows_reg_kernel(const Params p
     }
   const float s = scale_of(block_amax(a, red));
   if (threadIdx.x == 0) *(DAN_GLOBAL float *)(p.scale + r) = s;
-  uint8_t *out = p.xq + (int64_t)r * p.cols;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = 8 * threadIdx.x + j * 8 * kThreads;
-    if (c < p.cols) {
-      u32x2 q;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[j][4 * h] / s, x[j][4 * h + 1] / s, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(x[j][4 * h + 2] / s, x[j][4 * h + 3] / s, w, true);
-        q[h] = (uint32_t)w;
-      }
-      *(DAN_GLOBAL u32x2 *)(out + c) = q;
-    }
+    if (c < p.cols) *(DAN_GLOBAL u32x2 *)(p.xq + code_offset(p, r, c)) = codes8<T>(x[j], s);
   }
+  zero_row_tail(p, r);
 }
 
 // Per tensor, step 1: zero the accumulator (scale[0] holds amax's bits until step 3).
@@ -189,24 +215,30 @@ template <typename T>
 __global__ __launch_bounds__(kThreads) void quant_tensor_kernel(const Params p) {
   const float s = *(const DAN_GLOBAL float *)p.scale;
   const int r = blockIdx.x;
-  quantize_row<T>(static_cast<const T *>(p.x) + (int64_t)r * p.x_stride, p.xq + (int64_t)r * p.cols, p.cols, s);
+  if (pad_row(p, r)) return;
+  quantize_row<T>(p, static_cast<const T *>(p.x) + (int64_t)r * p.x_stride, r, s);
+  zero_row_tail(p, r);
 }
+
+// rows of codes written: the tiled layout pads to whole 256-row panels
+inline int out_rows(const Params &p) { return p.tiled ? (p.rows + 255) / 256 * 256 : p.rows; }
 
 template <typename T>
 hipError_t launch(const Params &p, int mode, hipStream_t s) {
   if (mode == DAN_FP8_SCALE_ROW) {
     const int chunks = (p.cols + 8 * kThreads - 1) / (8 * kThreads);
-    if (chunks <= 1) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 1>), dim3(p.rows), dim3(kThreads), 0, s, p);
-    else if (chunks <= 2) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 2>), dim3(p.rows), dim3(kThreads), 0, s, p);
-    else if (chunks <= 4) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 4>), dim3(p.rows), dim3(kThreads), 0, s, p);
-    else if (chunks <= 8) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 8>), dim3(p.rows), dim3(kThreads), 0, s, p);
-    else hipLaunchKernelGGL(quant_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+    const dim3 grid(out_rows(p));
+    if (chunks <= 1) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 1>), grid, dim3(kThreads), 0, s, p);
+    else if (chunks <= 2) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 2>), grid, dim3(kThreads), 0, s, p);
+    else if (chunks <= 4) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 4>), grid, dim3(kThreads), 0, s, p);
+    else if (chunks <= 8) hipLaunchKernelGGL((quant_rows_reg_kernel<T, 8>), grid, dim3(kThreads), 0, s, p);
+    else hipLaunchKernelGGL(quant_rows_kernel<T>, grid, dim3(kThreads), 0, s, p);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(1), 0, s, p.scale);
   hipLaunchKernelGGL(amax_rows_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
   hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1), 0, s, p.scale);
-  hipLaunchKernelGGL(quant_tensor_kernel<T>, dim3(p.rows), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL(quant_tensor_kernel<T>, dim3(out_rows(p)), dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 
@@ -215,6 +247,11 @@ hipError_t launch(const Params &p, int mode, hipStream_t s) {
 extern "C" {
 
 int dan_fp8_abi_version(void) { return DAN_FP8_ABI_VERSION; }
+
+int64_t dan_fp8_tiled_bytes(int32_t rows, int32_t cols) {
+  if (rows < 0 || cols < 0) return -1;
+  return (int64_t)((rows + 255) / 256) * 256 * ((cols + 63) / 64) * 64;
+}
 
 int dan_fp8_quantize(const DanFp8QuantArgs *a, void *stream) {
   using dan::fail;
@@ -226,6 +263,8 @@ int dan_fp8_quantize(const DanFp8QuantArgs *a, void *stream) {
     return fail(DAN_ERR_UNSUPPORTED, "dtype %d: bf16, f16 or f32", a->dtype);
   if (a->mode != DAN_FP8_SCALE_TENSOR && a->mode != DAN_FP8_SCALE_ROW)
     return fail(DAN_ERR_INVALID_ARGUMENT, "mode %d: 0 (tensor) or 1 (row)", a->mode);
+  if (a->layout != DAN_FP8_LAYOUT_ROWS && a->layout != DAN_FP8_LAYOUT_TILED)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "layout %d: 0 (rows) or 1 (tiled)", a->layout);
   if (a->rows < 0 || a->cols < 0) return fail(DAN_ERR_INVALID_ARGUMENT, "negative shape");
   if (a->cols % 16) return fail(DAN_ERR_INVALID_ARGUMENT, "cols %d must be a multiple of 16", a->cols);
   if (a->rows == 0 || a->cols == 0) {  // torch's amax of an empty tensor raises; an empty row list is a no-op
@@ -239,6 +278,8 @@ int dan_fp8_quantize(const DanFp8QuantArgs *a, void *stream) {
     return fail(DAN_ERR_INVALID_ARGUMENT, "x rows must be 16-byte aligned with x_stride >= cols, xq 16-byte aligned");
   dan_fp8::Params p;
   p.x = a->x; p.x_stride = a->x_stride; p.xq = a->xq; p.scale = a->scale; p.rows = a->rows; p.cols = a->cols;
+  p.tiled = a->layout == DAN_FP8_LAYOUT_TILED;
+  p.kt = (a->cols + 63) / 64;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   if (a->dtype == DAN_DTYPE_BF16) err = dan_fp8::launch<__bf16>(p, a->mode, s);

@@ -36,16 +36,32 @@ typedef enum {
   DAN_FP8_SCALE_ROW = 1     /* one scale per row (dan's default on sm90+) */
 } DanFp8ScaleMode;
 
+/* Layouts of e4m3 codes.
+ * ROWS:  [M, K] row-major, row stride K bytes.
+ * TILED: the GEMM's operand layout. Rows are padded to whole panels of 256
+ *        and K to whole k-steps of 64 bytes (padding holds zeros); panel p,
+ *        k-step s is 16 KB at ((p * KS + s) * 16 KB), KS = ceil(K / 64). It
+ *        holds 16 blocks of 16 rows x 64 bytes, block b (rows 16 b .. 16 b +
+ *        15 of the panel) at b * 1 KB; row i of a block sits at 64 i, its
+ *        16-byte chunk j (bytes 16 j .. 16 j + 15 of the k-step) at position
+ *        j ^ f(i), f(i) = ((i >> 1) & 3) ^ ((i >> 3) & 1). Each 1 KB block is
+ *        then one 16-byte-per-lane load of the GEMM, already in the order its
+ *        LDS stage wants. Size: dan_fp8_tiled_bytes(M, K). */
+typedef enum {
+  DAN_FP8_LAYOUT_ROWS = 0,
+  DAN_FP8_LAYOUT_TILED = 1
+} DanFp8Layout;
+
 typedef struct {
   int32_t abi_version; /* DAN_FP8_ABI_VERSION */
   int32_t dtype;       /* DanDtype of x: bf16, f16 or f32 */
   int32_t rows;        /* M */
   int32_t cols;        /* K: a multiple of 16 */
   int32_t mode;        /* DanFp8ScaleMode */
-  int32_t reserved;
+  int32_t layout;      /* DanFp8Layout of xq */
   const void *x;       /* [M, K], row stride x_stride elements, 16-byte aligned rows */
   int64_t x_stride;
-  uint8_t *xq;         /* [M, K] e4m3fn (OCP) codes, row-major, row stride K */
+  uint8_t *xq;         /* e4m3fn (OCP) codes in `layout`: [M, K] (ROWS) or dan_fp8_tiled_bytes(M, K) bytes (TILED) */
   float *scale;        /* [M] (rowwise) or [1] (tensor) fp32 */
 } DanFp8QuantArgs;
 
@@ -53,9 +69,12 @@ typedef struct {
  * Replaces dan/fused.py:85-91 (fp8_quantize) on gfx950. */
 int dan_fp8_quantize(const DanFp8QuantArgs *args, void *stream);
 
-/* Flags of DanFp8GemmArgs: a scale given per tensor (one value) instead of per row. */
+/* Flags of DanFp8GemmArgs: a scale given per tensor (one value) instead of
+ * per row; an operand in the TILED layout (its stride is then unused). */
 #define DAN_FP8_GEMM_X_SCALE_TENSOR 1
 #define DAN_FP8_GEMM_W_SCALE_TENSOR 2
+#define DAN_FP8_GEMM_X_TILED 4
+#define DAN_FP8_GEMM_W_TILED 8
 
 typedef struct {
   int32_t abi_version;  /* DAN_FP8_ABI_VERSION */
@@ -64,10 +83,10 @@ typedef struct {
   int32_t n;            /* rows of wq, columns of y (output features): a multiple of 16 */
   int32_t k;            /* columns of xq and wq (input features): a multiple of 16 */
   int32_t flags;        /* DAN_FP8_GEMM_* */
-  const uint8_t *xq;    /* [M, K] e4m3fn codes, row stride xq_stride bytes (16-byte aligned rows) */
+  const uint8_t *xq;    /* [M, K] e4m3fn codes, row stride xq_stride bytes (16-byte aligned rows), or TILED */
   int64_t xq_stride;
   const float *x_scale; /* [M] fp32, or [1] with DAN_FP8_GEMM_X_SCALE_TENSOR */
-  const uint8_t *wq;    /* [N, K] e4m3fn codes (the weight as stored, not transposed) */
+  const uint8_t *wq;    /* [N, K] e4m3fn codes (the weight as stored, not transposed), or TILED */
   int64_t wq_stride;
   const float *w_scale; /* [N] fp32 (16-byte aligned), or [1] with DAN_FP8_GEMM_W_SCALE_TENSOR */
   const void *bias;     /* [N] of out_dtype (16-byte aligned), or NULL */
@@ -80,6 +99,9 @@ typedef struct {
  * Replaces dan/quant.py:39-41 (torch._scaled_mm(xq, weight.t(), scale_a,
  * scale_b, bias, out_dtype) in FP8Linear.forward) on gfx950. */
 int dan_fp8_gemm(const DanFp8GemmArgs *args, void *stream);
+
+/* Bytes of an [rows, cols] e4m3 tensor in the TILED layout (-1 for a negative shape). */
+int64_t dan_fp8_tiled_bytes(int32_t rows, int32_t cols);
 
 int dan_fp8_abi_version(void);
 

@@ -74,8 +74,9 @@ def test_ctypes_layout_matches_header(tmp_path):
                  'DAN_FRONT_NORM_RMS_ZERO_CENTERED);')
     lines.append('printf("PLAN %d,%d,%d,%d,%d\\n", DAN_TREE_PLAN_ABI_VERSION, DAN_TREE_PLAN_MAX_WORK, '
                  'DAN_TREE_PLAN_MAX_SLOTS, DAN_TREE_PLAN_MAX_SEGMENTS, DAN_TREE_PLAN_MAX_BRANCHES);')
-    lines.append('printf("FP8 %d,%d,%d,%d,%d\\n", DAN_FP8_ABI_VERSION, DAN_FP8_SCALE_TENSOR, DAN_FP8_SCALE_ROW, '
-                 'DAN_FP8_GEMM_X_SCALE_TENSOR, DAN_FP8_GEMM_W_SCALE_TENSOR);')
+    lines.append('printf("FP8 %d,%d,%d,%d,%d,%d,%d,%d,%d\\n", DAN_FP8_ABI_VERSION, DAN_FP8_SCALE_TENSOR, DAN_FP8_SCALE_ROW, '
+                 'DAN_FP8_GEMM_X_SCALE_TENSOR, DAN_FP8_GEMM_W_SCALE_TENSOR, DAN_FP8_GEMM_X_TILED, DAN_FP8_GEMM_W_TILED, '
+                 'DAN_FP8_LAYOUT_ROWS, DAN_FP8_LAYOUT_TILED);')
     lines.append('printf("GDN %d\\n", DAN_GDN_ABI_VERSION);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
@@ -96,7 +97,9 @@ def test_ctypes_layout_matches_header(tmp_path):
     assert got["FRONT"] == (f"{_native.FRONT_ABI_VERSION},{_native.FRONT_NORM_NONE},{_native.FRONT_NORM_RMS},"
                             f"{_native.FRONT_NORM_RMS_ZERO_CENTERED}")
     assert got["FP8"] == (f"{_native.FP8_ABI_VERSION},{_native.FP8_SCALE_TENSOR},{_native.FP8_SCALE_ROW},"
-                          f"{_native.FP8_GEMM_X_SCALE_TENSOR},{_native.FP8_GEMM_W_SCALE_TENSOR}")
+                          f"{_native.FP8_GEMM_X_SCALE_TENSOR},{_native.FP8_GEMM_W_SCALE_TENSOR},"
+                          f"{_native.FP8_GEMM_X_TILED},{_native.FP8_GEMM_W_TILED},"
+                          f"{_native.FP8_LAYOUT_ROWS},{_native.FP8_LAYOUT_TILED}")
     assert int(got["GDN"]) == _native.GDN_ABI_VERSION
     assert got["PLAN"] == (f"{_native.PLAN_ABI_VERSION},{_native.PLAN_MAX_WORK},{_native.PLAN_MAX_SLOTS},"
                            f"{_native.PLAN_MAX_SEGMENTS},{_native.PLAN_MAX_BRANCHES}")

@@ -171,3 +171,29 @@ def test_planted_model_mistakes_fail(monkeypatch):
             results = (_sum([1.0, 2.0 ** -9], [1.0, 2.0 ** -5]),
                        _sum([1.0] + [2.0 ** -9] * 63, [1.0] + [2.0 ** -9] * 63))
             assert results != (1.0, 1 + 56 * 2.0 ** -18), name
+
+
+def test_tiled_layout_closed_forms():
+    """The tiled layout's offsets at hand-computed positions, padding zeros,
+    and every code placed exactly once."""
+    rows, cols = 300, 208  # 2 panels, 4 k-steps (the last one 16 bytes wide)
+    codes = np.random.default_rng(2).integers(1, 255, size=(rows, cols), dtype=np.uint8)
+    t = Q.tile_e4m3(codes)
+    ks = 4
+    assert t.size == 512 * 256
+    assert t[0] == codes[0, 0] and t[64] == codes[1, 0]       # row 1: f(1) = 0
+    assert t[128 + 16] == codes[2, 0]                          # row 2: f(2) = 1, chunk 0 at position 1
+    assert t[8 * 64 + 16 * 1] == codes[8, 0]                    # row 8: f(8) = 1
+    assert t[1024] == codes[16, 0]                              # block 1 of the panel
+    assert t[16384] == codes[0, 64]                             # k-step 1
+    assert t[ks * 16384] == codes[256, 0]                        # panel 1
+    assert t[16 * 1] == codes[0, 16] and t[64 + 16 * 3] == codes[1, 48]
+    # a bijection onto the non-padding positions: tile index planes and read each element back
+    r, k = np.meshgrid(np.arange(rows), np.arange(cols), indexing="ij")
+    planes = [Q.tile_e4m3(v.astype(np.uint8)) for v in (r % 256, r // 256, k % 256, k // 256, np.ones_like(r))]
+    used = planes[4] == 1
+    assert used.sum() == rows * cols and (t[~used] == 0).all()
+    back_r = planes[0][used].astype(int) + 256 * planes[1][used].astype(int)
+    back_k = planes[2][used].astype(int) + 256 * planes[3][used].astype(int)
+    assert len(set(zip(back_r.tolist(), back_k.tolist()))) == rows * cols
+    assert np.array_equal(t[used], codes[back_r, back_k])

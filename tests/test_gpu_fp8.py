@@ -132,6 +132,29 @@ def test_fp8_linear_equals_dan_formulation_and_oracle(gpu):
                 say(f"  {name}: max |y - exact| {err.max().item():.3e}")
 
 
+def test_fp8_linear_retiles_a_changed_weight(gpu):
+    """FP8Linear streams a tiled copy of its weight; writing new codes into
+    `weight` in place (as a state-dict load does) makes the next forward use
+    them."""
+    say("FP8Linear: re-tiling after an in-place weight change")
+    g = torch.Generator().manual_seed(21)
+    lin = nn.Linear(512, 256, bias=False).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(256, 512, generator=g) * 0.02)
+    f = DQ.FP8Linear(lin.to(gpu))
+    x = torch.randn(300, 512, generator=g).to(torch.bfloat16).to(gpu)
+    y0 = f(x)
+    other, _ = DQ.fp8_quantize((torch.randn(256, 512, generator=g) * 0.02).to(torch.bfloat16).to(gpu))
+    with torch.no_grad():
+        f.weight.copy_(other)
+    y1 = f(x)
+    xq, sx = DQ.fp8_quantize(x)
+    want = DQ.fp8_gemm(xq, sx, other, f.weight_scale, None, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert not torch.equal(y0, y1)
+    assert torch.equal(y1, want)
+
+
 def test_module_replacement_and_errors(gpu):
     class Layer(nn.Module):
         def __init__(self):

@@ -24,6 +24,7 @@ Llama-3-8B layer's full shapes against the same float64 expressions
 evaluated on the GPU."""
 import sys
 
+import numpy as np
 import pytest
 import torch
 
@@ -236,3 +237,41 @@ def test_gemm_errors(gpu):
     y = DQ.fp8_gemm(xq, s1, wq, s1.reshape(1, 1))  # per-tensor scales, zero operands
     torch.cuda.synchronize()
     assert (y == 0).all()
+
+
+@pytest.mark.parametrize("m,k", [(1, 16), (300, 208), (256, 4096), (513, 4112), (40, 14336)])
+@pytest.mark.parametrize("rowwise", [True, False])
+def test_quantizer_tiled_output_matches_oracle_layout(gpu, m, k, rowwise):
+    """The quantizer's tiled codes equal the oracle's codes placed by the
+    oracle's layout (oracle/quant.py tile_e4m3), zero padding included; the
+    device re-tiling of row-major codes (dan_amd.quant.tile_codes) agrees."""
+    say(f"fp8 quantize tiled M {m} K {k} {'rowwise' if rowwise else 'per tensor'}")
+    g = torch.Generator().manual_seed(m + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    t, s = DQ.fp8_quantize(x.to(gpu), rowwise=rowwise, tiled=True)
+    rq, rs = OQ.fp8_quantize(x, rowwise)
+    want = OQ.tile_e4m3(rq.view(torch.uint8).numpy())
+    torch.cuda.synchronize()
+    assert t.shape == (m, k) and t.data.numel() == want.size
+    assert torch.equal(s.cpu(), rs)
+    assert np.array_equal(t.data.cpu().numpy(), want)
+    assert np.array_equal(DQ.tile_codes(rq.to(gpu)).data.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 1024), (257, 272, 48), (513, 784, 4112), (255, 528, 208),
+                                   (64, 128, 576), (8192, 4096, 4096)])
+def test_tiled_operands_give_identical_results(gpu, m, n, k):
+    """Tiled and row-major operands, in every combination, give the same bits
+    (the same products in the same order); covers both the persistent kernel
+    (even k-step counts >= 6) and the per-tile kernel (K 48, 208, 576, 4112)."""
+    say(f"fp8 GEMM tiled operands M {m} N {n} K {k}")
+    g = torch.Generator().manual_seed(3 * m + n + k)
+    xq, sx, wq, sw = (t.to(gpu) for t in operands(m, n, k, g))
+    bias = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    xt, wt = DQ.tile_codes(xq), DQ.tile_codes(wq)
+    ref = DQ.fp8_gemm(xq, sx, wq, sw, bias, torch.bfloat16)
+    for xa, wa, name in ((xt, wq, "x tiled"), (xq, wt, "w tiled"), (xt, wt, "both tiled")):
+        y = DQ.fp8_gemm(xa, sx, wa, sw, bias, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), name
+    say("  identical for x tiled, w tiled and both")
