@@ -11,8 +11,11 @@
 //
 // Shape of the computation (one work group per 256 x 256 tile of y, four
 // waves, each wave a 128 x 128 quarter):
-// - Both operands are K-major byte rows: xq [M, K] and wq [N, K] as dan
-//   stores them (the weight is never transposed).
+// - Both operands are K-major: xq [M, K] and wq [N, K] as dan stores them
+//   (the weight is never transposed), either as byte rows at a stride or in
+//   the tiled layout of include/dan_fp8.h, where each 256-row panel's 64-byte
+//   k-step is 16 contiguous KB already in the LDS order below, so every direct
+//   load reads one contiguous KB.
 // - Products run on v_mfma_f32_32x32x64_f8f6f4 (OCP e4m3 x e4m3, fp32
 //   accumulate; 64 k per instruction). The matrix core's A operand is a
 //   32-row block of w and its B operand a 32-row block of x, so each lane's
