@@ -33,9 +33,10 @@
 //                                softmax state; row max/sum need one cross-half
 //                                exchange.
 //   online softmax in fp32 with exp2 (scale * log2 e folded in); the running
-//   max is not recomputed per tile, only raised when a tile's largest score
-//   would put p above 2^kLog2Limit (fp16's range), so the O accumulators are
-//   rarely rescaled.
+//   max is not recomputed per tile. It stays at the first tile's max unless a
+//   later p overflows fp16, in which case the unit runs again raising m per
+//   tile whenever a score would put p above 2^kLog2Limit, so the O
+//   accumulators are rarely rescaled and most tiles skip the max altogether.
 //   O^T[d, query] += V^T P^T     v_mfma_f32_32x32x16_f16: A = V^T rows from LDS,
 //                                B = P^T straight from the S^T registers: K rows
 //                                are staged in a permuted order that makes the
@@ -84,6 +85,7 @@ inline int waves_for(int head_dim) { return head_dim == 256 ? Shape<256>::waves 
 // apart.
 constexpr int kIssuers = 4;
 constexpr float kLog2Limit = 15.0f;  // p = exp2(S c - m) <= 2^15: P stays inside fp16's range
+constexpr int kVoteBytes = 16;       // LDS past the stage ring: the work group's overflow votes
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -477,7 +479,7 @@ struct Lds {
   static constexpr int kRowsPerPeriod = kRowBytes >= 256 ? 1 : 256 / kRowBytes;
   static constexpr int kSwizzle = kChunks < 16 ? kChunks : 16;
   static_assert(kBytes % 1024 == 0 && vBytes % 1024 == 0, "whole 1 KB blocks");
-  static_assert(total <= 160 * 1024, "LDS");
+  static_assert(total + kVoteBytes <= 160 * 1024, "LDS");
   // Operand reads XOR the chunk into (buffer offset + lane offset): the
   // buffer offsets must leave the lane offset's bits (32 rows) untouched.
   static_assert(buf % (32 * kRowBytes) == 0, "buffer alignment");
@@ -789,6 +791,19 @@ void tree_attn_kernel(const KParams args) {
   // pipeline does not drain between units. `pre` counts the current unit's
   // tiles the previous unit issued.
   int gbase = 0, pre = 0;
+  // Passes over units (a unit run again with the check is a second pass);
+  // each pass votes in LDS word pass % 2, past the stage ring.
+  int pass = 0;
+  bool check = false;
+  auto vote_word = [&](int k) __attribute__((always_inline)) -> volatile DAN_LDS uint32_t & {
+    return *(volatile DAN_LDS uint32_t *)(uintptr_t)(smem_lds + (uint32_t)L::total + 4u * (uint32_t)(k & 1));
+  };
+  if constexpr (!kTwoStage) {
+    if (tid == 0) {
+      vote_word(0) = 0u;
+      vote_word(1) = 0u;
+    }
+  }
   // A wave's q fragments and key_lo for a unit: loaded in the unit's
   // prologue, or, when the previous unit ran here, during that unit's last
   // step (where they are no longer used), so the prologue does not wait a
@@ -979,11 +994,16 @@ void tree_attn_kernel(const KParams args) {
     // Softmax of one tile (VALU): P = exp2(S * c - m) in fp16 and the lane's
     // partial row sum of the fp16-rounded values that P V uses (exact products,
     // fp32 accumulation), so rounding P mostly cancels in O / l. The running
-    // max m is not recomputed per tile: before a tile's exponentials, a lane
-    // score above m + kLog2Limit (or a NaN) in any lane raises m to the tile's
-    // max (O and l rescaled), so every p stays below 2^15. The check reads S
-    // only, so P V does not wait on the row sum. A lane holds half of its
-    // query's keys and the other half sits in lane ^ 32; both keep the same m.
+    // max m is not recomputed per tile. A unit's first pass keeps m at the
+    // first tile's max: p may then exceed 2^15 (fine) or overflow fp16 to inf,
+    // which the row sum shows at the unit's end, and the work group runs the
+    // unit again with the check (two ring-of-four passes; the two-buffer
+    // instantiation always checks). With the check, a lane score above
+    // m + kLog2Limit (or a NaN) in any lane raises m to the tile's max (O and l
+    // rescaled) before the tile's exponentials, so every p stays below 2^15;
+    // the check reads S only, so P V does not wait on the row sum. A lane
+    // holds half of its query's keys and the other half sits in lane ^ 32;
+    // both keep the same m.
     // max S over the lane's 32 keys: a tree of three-input maxima (v_max3_f32,
     // two values per instruction): 32 -> 12 -> 4 -> 1 in 16 instructions.
     auto lane_max = [&](const f32x16(&s)[2]) __attribute__((always_inline)) {
@@ -1030,8 +1050,12 @@ void tree_attn_kernel(const KParams args) {
     // put p above 2^kLog2Limit, and bring O to the scale of the tile's V^T
     // block (2^ve) if it differs from O's (2^vE). Both are rare and share one
     // branch.
-    auto begin_tile = [&](const f32x16(&s)[2], float c, int ve) __attribute__((always_inline)) {
-      const bool raise = __any(!(fmaf(lane_max(s), c, mneg) <= kLog2Limit));
+    // Without the check (kCheck false) no score raises m: a p that overflows
+    // fp16 becomes inf, which the row sum carries to the unit's end, where
+    // the work group then runs the unit again with the check (see the vote).
+    auto begin_tile = [&](bool chk, const f32x16(&s)[2], float c, int ve) __attribute__((always_inline)) {
+      bool raise = false;
+      if (chk) raise = __any(!(fmaf(lane_max(s), c, mneg) <= kLog2Limit));
       if (raise || ve != vE) {
         float f = exp2i(vE - ve);
         if (raise) {
@@ -1123,7 +1147,7 @@ void tree_attn_kernel(const KParams args) {
         fix_straddle(tile_of(it), s);
         const float c = tile_c(tile_of(it));
         if (it == 0) mneg = -fmaxf(s_max(s) * c, -3.0e38f);
-        begin_tile(s, c, ve);
+        begin_tile(true, s, c, ve);
         lsum += exp_phase(s, c);
         pv_phase((gbase + it) & (NB - 1));
       }
@@ -1145,14 +1169,18 @@ void tree_attn_kernel(const KParams args) {
       q_ready = false;
       wait_vmem<0>();
       barrier_lds();
+      // Every wave has read the previous pass's vote: its word is the next
+      // pass's, cleared now.
+      if (tid == 0) vote_word(pass + 1) = 0u;
       f32x16 sc[2];  // S of the current tile
       // The running max m starts at the largest visible score of the first
       // tile (exact, so that tile's largest p is 1). A query that sees no key
       // of the first tile (only when the segment has neither past nor trunk)
       // starts from m = -3e38: its p stay 0 while its keys are hidden, and its
-      // first visible key scores far above m + kLog2Limit, which raises m to
-      // that tile's max (O and l are still 0, scaled by exp2(-3e38 - m) = 0).
-      // Finite throughout, so no inf - inf.
+      // first visible key scores far above m + kLog2Limit, which overflows
+      // without the check and, with it, raises m to that tile's max (O and l
+      // are still 0, scaled by exp2(-3e38 - m) = 0). Finite throughout, so no
+      // inf - inf.
       qk_phase(gbase & (NB - 1), sc, [](int) {});
       mask_phase(tile_of(0), sc);
       fix_straddle(tile_of(0), sc);
@@ -1182,7 +1210,7 @@ void tree_attn_kernel(const KParams args) {
           q_ready = true;
         }
         const float c = tile_c(tile_of(it));
-        begin_tile(s, c, ve);
+        begin_tile(check, s, c, ve);
         const float ts = exp_phase(s, c);
         if (!kLast) qk_phase((gbase + it + 1) & (NB - 1), s, [](int) {});
         lsum += ts;
@@ -1197,6 +1225,33 @@ void tree_attn_kernel(const KParams args) {
       using Last = std::integral_constant<bool, true>;
       while (it + 1 < ntile) step(NotLast{}, sc);
       step(Last{}, sc);
+      // The overflow vote. A pass without the check is exact unless some p
+      // overflowed fp16 (a score about 16 above the running max, or a NaN):
+      // then that query's row sum is inf or NaN. If any valid query of the
+      // work group has one, the work group runs the unit again with the
+      // check, after its loads have landed (the next unit's first tiles are
+      // issued again by that pass).
+      if (!check) {
+        const float lt = lsum + __shfl_xor(lsum, 32);
+        const bool bad = qvalid && (__builtin_bit_cast(uint32_t, lt) & 0x7f800000u) == 0x7f800000u;
+        if (__any(bad) && lane == 0) vote_word(pass) = 1u;
+        barrier_lds();
+        const bool replay = __builtin_amdgcn_readfirstlane(vote_word(pass)) != 0u;
+        ++pass;
+        if (replay) {
+          wait_vmem<0>();
+          barrier_lds();
+          check = true;
+          q_ready = false;
+          gbase += ntile;
+          pre = 0;
+          --u;
+          continue;
+        }
+      } else {
+        ++pass;
+        check = false;
+      }
     }
 
     // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
@@ -1358,7 +1413,7 @@ hipError_t launch_pack(const PackParams &pp, int blocks, hipStream_t stream) {
 template <typename TQK, typename TOut, int D>
 hipError_t launch_attn(const KParams &kp, int grid, hipStream_t stream) {
   auto kernel = tree_attn_kernel<TQK, TOut, D>;
-  constexpr int lds = Lds<D, (int)sizeof(TQK)>::total;
+  constexpr int lds = Lds<D, (int)sizeof(TQK)>::total + kVoteBytes;
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (attr != hipSuccess) return attr;

@@ -160,6 +160,46 @@ def test_running_max_raised_by_growing_scores(gpu):
     check(w, "growing scores")
 
 
+def _as_dtype(w, dtype):
+    return W.Workload(f"{w.name}-{dtype}", w.q.to(dtype), w.k.to(dtype), w.v.to(dtype), w.segments, w.layer, {})
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "e4m3"])
+def test_overflowing_units_among_others(gpu, dtype):
+    """The kernel runs a unit without the per-tile overflow check and runs it
+    again with the check when a probability overflowed fp16. Here the first
+    segment's scores grow along its 600-token trunk (its units overflow and
+    run twice) while the other segments' scores are flat (one pass), so work
+    groups mix both kinds and a second pass sits between units whose first
+    tiles were prefetched."""
+    structure = [(600, [40, 24]), (600, [30]), (300, [20, 20]), (200, [])]
+    first = 600 + 64
+
+    def scores(t):
+        b = np.where(t < first, 0.1 * t, 0.5).astype(np.float32)
+        return np.full(t.shape, 4.0, np.float32), b
+    w = _scored_batch(gpu, structure, scores)
+    if dtype == "e4m3":
+        _fp8_case(w, "overflowing units among others (e4m3)", gpu, vs_original=False)
+        return
+    check(w if dtype == "fp32" else _as_dtype(w, torch.bfloat16), f"overflowing units among others ({dtype})")
+
+
+@pytest.mark.parametrize("rise", [15.5, 16.5])
+def test_probabilities_near_fp16_limit(gpu, rise):
+    """Keys 0-63 score 0 and every later key scores `rise` (log2 units) above
+    them, so queries past the first tile start from m = 0 and then meet
+    p = 2^rise: 2^15.5 fits fp16 (one pass, P up to 46341), 2^16.5 overflows
+    it (the unit runs again with the check, which raises m)."""
+    d = 128
+    raw = rise / (math.log2(math.e) / math.sqrt(d))  # raw q.k giving S * scale * log2(e) = rise
+
+    def scores(t):
+        return np.full(t.shape, 4.0, np.float32), np.where(t < 64, 0.0, raw / 4.0).astype(np.float32)
+    w = _scored_batch(gpu, [(300, [40, 24])], scores, d=d)
+    check(w, f"probabilities near the fp16 limit (rise {rise})")
+
+
 def dequantized(w):
     """An e4m3 workload with q, k, v and every cache entry dequantized to fp32
     (x = xq * scale), for the oracle."""
