@@ -15,11 +15,14 @@
 //
 // Numerics are those of the eager torch ops the reference runs: fp32
 // arithmetic, each op's result rounded to the storage type (RNE):
-//   RMS:            n = rnd(w * rnd(x * r)),   r = 1 / sqrt(sum(x^2) / D + eps)
+//   RMS:            n = rnd(w * rnd(x * r)),   r = rsqrt(sum(x^2) / D + eps)
 //   zero-centered:  n = rnd(x * r * (1 + w))
 //   rotate-half:    o = rnd(rnd(n * cos) + rnd(rot(n) * sin)),
 //                   rot(n)[i] = -n[i + R/2] for i < R/2, n[i - R/2] for R/2 <= i < R
-// The only difference from torch is the summation order of sum(x^2).
+// The differences from torch are the summation order of sum(x^2) and r,
+// which is the hardware rsqrt (within 1 ulp of the fp32 1 / sqrt): without a
+// norm the outputs are bit-identical, with one an element moves by at most
+// one unit of the storage type, rarely (a few per million at the Llama shape).
 //
 // The kernel is HBM-bound: it reads q, k (and the saved v rows) and cos /
 // sin once and writes q, k (and the saves) once.
@@ -27,6 +30,11 @@
 #include <stdint.h>
 
 #include "dan_qkv_front.h"
+
+// Every eager op rounds its result to the storage type, so a product followed
+// by a sum must not be fused: contraction would drop the rounding of the
+// product (rnd(n * cos) + rnd(rot * sin) would become fma(n, cos, ...)).
+#pragma clang fp contract(off)
 
 namespace dan {
 int fail(int status, const char *fmt, ...);  // tree_attn.hip: sets the thread's last-error message
@@ -63,10 +71,11 @@ template <typename T>
 __device__ inline u32x4 from_f32(f32x8 x) {
   return __builtin_bit_cast(u32x4, __builtin_convertvector(x, typename Vec8<T>::type));
 }
-// The result of one eager op: an fp32 value rounded to the storage type.
+// The result of one eager op on 8 values: fp32 rounded to the storage type
+// (two values per conversion instruction) and widened back.
 template <typename T>
-__device__ inline float rnd(float x) {
-  return (float)(T)x;
+__device__ inline f32x8 rnd8(f32x8 x) {
+  return to_f32<T>(from_f32<T>(x));
 }
 
 template <typename T>
@@ -109,7 +118,7 @@ struct Params {
 // Head vectors per lane (qkv_front_kernel).
 constexpr int kVecs = 2;
 
-template <typename T, int D>
+template <typename T, int D, int NORM>
 __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
   constexpr int L = D / 8;      // lanes per head vector
   constexpr int VPB = 256 / L;  // head vectors per work group and pass
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
       // lane's own x, where the norm weight or the rotary tables are unused):
       // loads under branches would make the compiler wait for each in turn.
       const T *row = src + 8 * j;
-      const T *wrow = p.norm != DAN_FRONT_NORM_NONE ? static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j : row;
+      const T *wrow = NORM != DAN_FRONT_NORM_NONE ? static_cast<const T *>(isq ? p.qw : p.kw) + 8 * j : row;
       const int64_t cs_off = (int64_t)tc * p.cs_st + min(8 * j, p.R - 8);
       const T *crow = p.R > 0 ? static_cast<const T *>(p.cos) + cs_off : row;
       const T *srow = p.R > 0 ? static_cast<const T *>(p.sin) + cs_off : row;
@@ -168,17 +177,15 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
     const f32x8 x = to_f32<T>(xraw[k]), w = to_f32<T>(wraw[k]), cs = to_f32<T>(craw[k]), sn = to_f32<T>(sraw[k]);
 
     f32x8 n = x;
-    if (p.norm != DAN_FRONT_NORM_NONE) {
+    if constexpr (NORM != DAN_FRONT_NORM_NONE) {
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
       ss = vec_sum<L>(ss);
-      const float r = 1.0f / __builtin_sqrtf(ss / (float)D + p.eps);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float y = x[i] * r;
-        n[i] = p.norm == DAN_FRONT_NORM_RMS ? rnd<T>(w[i] * rnd<T>(y)) : rnd<T>(y * (1.0f + w[i]));
-      }
+      // rsqrt on the transcendental unit (within 1 ulp of 1 / sqrt, as torch's GPU rsqrt)
+      const float r = __builtin_amdgcn_rsqf(ss * (1.0f / (float)D) + p.eps);
+      const f32x8 y = x * r;
+      n = NORM == DAN_FRONT_NORM_RMS ? rnd8<T>(w * rnd8<T>(y)) : rnd8<T>(y * (1.0f + w));
     }
 
     f32x8 o = n;
@@ -186,18 +193,16 @@ __global__ __launch_bounds__(256) void qkv_front_kernel(const Params p) {
       const int half = p.R / 16;  // lanes per rotary half
       const int partner = j < half ? j + half : j - half;
       const u32x4 np = from_f32<T>(n);  // exact: n is already rounded to T
+      // rot(n): the partner's values, negated in the first half (the sign
+      // bit of each 16-bit value, exact)
+      const uint32_t sign = j < half ? 0x80008000u : 0u;
       u32x4 pp;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const uint32_t word = np[c];
-        pp[c] = (uint32_t)__shfl((int)word, partner, L);  // lane `partner` of this vector's L lanes
+        pp[c] = (uint32_t)__shfl((int)word, partner, L) ^ sign;  // lane `partner` of this vector's L lanes
       }
-      const f32x8 pv = to_f32<T>(pp);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float rot = j < half ? -pv[i] : pv[i];
-        o[i] = rnd<T>(rnd<T>(n[i] * cs[i]) + rnd<T>(rot * sn[i]));
-      }
+      o = rnd8<T>(n * cs) + rnd8<T>(to_f32<T>(pp) * sn);  // rounded once more at the store
     }
     if (!okv[k]) continue;
     const u32x4 out = from_f32<T>(o);
@@ -224,8 +229,11 @@ template <typename T, int D>
 hipError_t launch(const Params &p, hipStream_t s) {
   constexpr int VPB = kVecs * (256 / (D / 8));  // head vectors per work group
   const int64_t vectors = (int64_t)p.N * (p.H + p.Hkv);
-  const int64_t grid = (vectors + VPB - 1) / VPB;
-  hipLaunchKernelGGL((qkv_front_kernel<T, D>), dim3((unsigned)grid), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)((vectors + VPB - 1) / VPB));
+  if (p.norm == DAN_FRONT_NORM_RMS) hipLaunchKernelGGL((qkv_front_kernel<T, D, DAN_FRONT_NORM_RMS>), grid, dim3(256), 0, s, p);
+  else if (p.norm == DAN_FRONT_NORM_RMS_ZERO_CENTERED)
+    hipLaunchKernelGGL((qkv_front_kernel<T, D, DAN_FRONT_NORM_RMS_ZERO_CENTERED>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((qkv_front_kernel<T, D, DAN_FRONT_NORM_NONE>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -3,12 +3,14 @@ CPU oracle (oracle/front.py) on identical seeded inputs.
 
 Bars: without a norm the chain is elementwise with the same op order and
 rounding as the eager torch ops, so the outputs must be bit-identical. With a
-norm, the only difference is the summation order of sum(x^2), which can move
-a normalized value by one rounding step; through the rotation that is at
-most one spacing of the largest value of its head row (where x*cos and
-rot*sin cancel, many spacings of the small result). Outputs must be within
-that of the oracle everywhere and bit-identical for at least 99.9 % of the
-elements. Saved rows are bit-identical to the kernel's own outputs."""
+norm, the factor r = rsqrt(mean(x^2) + eps) may differ from the oracle's in
+its last bit (the summation order of sum(x^2), and the hardware rsqrt, within
+1 ulp). That can move each normalized value by one rounding step. A rotated
+output adds two of them (rnd(n cos) + rnd(rot(n) sin)), so it moves by at
+most two spacings of the largest value of its head row (where the terms
+cancel, many spacings of the small result). Outputs must be within that of
+the oracle everywhere and bit-identical for at least 99.9 % of the elements.
+Saved rows are bit-identical to the kernel's own outputs."""
 import sys
 
 import pytest
@@ -67,7 +69,7 @@ def check(out, ref, exact):
     if exact:
         assert frac == 1.0
     else:
-        assert worst_row <= 1.0 and frac >= 0.999
+        assert worst_row <= 2.0 and frac >= 0.999
 
 
 def run_case(gpu, n, h, hkv, d, r, norm, dtype=torch.bfloat16, gate=False, seed=0):
