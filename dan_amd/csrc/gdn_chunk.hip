@@ -42,7 +42,9 @@ namespace dan_gdnc {
 constexpr int kC = DAN_GDN_CHUNK;  // tokens per chunk
 constexpr int kDk = 128;
 constexpr int kThreads = 256;
-constexpr int kCols = 32;  // state columns per scan work group
+// State columns per scan work group (a template argument of the scan: 32 or
+// 16) for phases of long and of short runs.
+constexpr int kLongCols = 16, kShortCols = 32;
 // Floats per (slot, value head): T [64][64], A [64][64], then five rows of 64:
 // beta gamma r_k, beta, r_q Dk^-1/2 gamma, exp(G_63 - G) r_k, {gamma_63, 0, ..}.
 constexpr int kRec = 2 * kC * kC + 5 * kC;
@@ -227,17 +229,25 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
 }
 
 // ---------------------------------------------------------------- the scan over chunks
-// LDS (floats): the state slice twice (the chunk's S and the next), [128][34]
-// each; Y, D and diag(exp(G_63 - G) r_k) D, [64][36] each. With these row
-// strides every B-operand read of v_mfma_f32_16x16x4_f32 (4 rows x 16
-// columns: rows 8 apart in S, 4 apart in the others) hits 64 distinct banks.
-constexpr int kSS = 34, kSB = 36;
-constexpr int kLds = 2 * kDk * kSS + 3 * kC * kSB;
-// The scan runs as 8 waves (one 16 x 16 tile each; for long runs, where a
-// chunk step's latency sets the pace) or as 4 waves (16 x 32 each; two work
-// groups per CU, for phases of many short runs, where the per-group fixed
-// cost does).
-constexpr int kScanLongWaves = 8, kScanShortWaves = 4;
+// LDS (floats) of a COLS-column scan: the state slice twice (the chunk's S
+// and the next), [128][COLS + 2] each; Y, D and diag(exp(G_63 - G) r_k) D,
+// [64][COLS + 4] each. With these row strides every B-operand read of
+// v_mfma_f32_16x16x4_f32 (4 rows x 16 columns: rows 8 apart in S, 4 apart in
+// the others) hits 64 distinct banks: 8 (COLS + 2) and 4 (COLS + 4) are 16
+// modulo 64 for COLS = 16 and 32.
+template <int COLS>
+struct ScanLds {
+  static constexpr int kSS = COLS + 2, kSB = COLS + 4;
+  static constexpr int floats = 2 * kDk * kSS + 3 * kC * kSB;
+  static_assert((8 * kSS) % 64 == 16 && (4 * kSB) % 64 == 16, "conflict-free operand reads");
+};
+// Long runs, where a chunk step's latency sets the pace: 4 waves on 16 state
+// columns (one 16 x 16 tile each), so a (run, head) spreads over 8 work groups.
+// Many short runs, where the per-group fixed cost does: 4 waves on 32 columns
+// (16 x 32 each). Both leave room for two work groups per CU. (The kernel
+// also runs as 8 waves on 32 columns, one tile each, which took 11 % longer on
+// a trunk phase of 5 runs of 286 to 1843 tokens.)
+constexpr int kScanLongWaves = 4, kScanShortWaves = 4;
 
 __device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
@@ -280,10 +290,13 @@ struct Ops {
 //   phase 2  O = (Q S) + A D (blocks j <= min(rb, jmax)), S <- gamma S + K^T Ds
 //            (blocks j <= jmax) into the other state buffer        barrier
 // A wave whose rows are all padding skips phases 0-1 and the O products.
-template <typename T, int W>
+template <typename T, int W, int COLS>
 __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
-  constexpr int NC = 8 / W;
-  __shared__ __attribute__((aligned(16))) float smem[kLds];
+  // 16-column halves per wave: 8 waves x 1 (32 columns), 4 x 2 (32), 4 x 1 (16)
+  constexpr int NC = COLS / 16 * 4 / W;
+  static_assert(NC >= 1 && (W == 4 || (W == 8 && COLS == 32)), "scan shapes");
+  constexpr int kCols = COLS, kSS = ScanLds<COLS>::kSS, kSB = ScanLds<COLS>::kSB;
+  __shared__ __attribute__((aligned(16))) float smem[ScanLds<COLS>::floats];
   // work group b -> (unit u = r Hv + h, column block cb); the ncb groups of a
   // unit share b % 8 and so an XCD, whose L2 then serves their common reads
   const int b = blockIdx.x;
@@ -491,22 +504,27 @@ hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t 
   p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
   p.rec = records;
   p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
-  p.ncb = a->v_dim / dan_gdnc::kCols; p.units = a->num_runs * a->num_v_heads;
+  p.units = a->num_runs * a->num_v_heads;
   const int64_t prep = dan_gdnc::slots(a->num_tokens, a->num_runs) * a->num_v_heads;
-  const int64_t scan = ((int64_t)p.units + 7) / 8 * 8 * p.ncb;
-  // Runs of DAN_GDN_SHORT_RUN tokens or fewer on average: the 4-wave scan
-  // (two work groups per CU); longer: the 8-wave scan (shorter chunk steps).
+  // Runs of DAN_GDN_SHORT_RUN tokens or fewer on average: the short-run scan;
+  // longer: the long-run scan.
   const bool shortrun = (int64_t)a->num_tokens <= (int64_t)DAN_GDN_SHORT_RUN * a->num_runs;
   const dim3 block(dan_gdnc::kThreads);
-  const dim3 sblock(64 * (shortrun ? dan_gdnc::kScanShortWaves : dan_gdnc::kScanLongWaves));
+  auto scan = [&](auto kernel, int waves, int cols) {
+    p.ncb = a->v_dim / cols;
+    const int64_t groups = ((int64_t)p.units + 7) / 8 * 8 * p.ncb;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)groups), dim3(64 * waves), 0, s, p);
+  };
+  constexpr int LW = dan_gdnc::kScanLongWaves, LC = dan_gdnc::kLongCols;
+  constexpr int SW = dan_gdnc::kScanShortWaves, SC = dan_gdnc::kShortCols;
   if (a->dtype == DAN_DTYPE_BF16) {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<__bf16>, dim3((unsigned)prep), block, 0, s, p);
-    if (shortrun) hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<__bf16, dan_gdnc::kScanShortWaves>), dim3((unsigned)scan), sblock, 0, s, p);
-    else hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<__bf16, dan_gdnc::kScanLongWaves>), dim3((unsigned)scan), sblock, 0, s, p);
+    if (shortrun) scan(dan_gdnc::chunk_scan_kernel<__bf16, SW, SC>, SW, SC);
+    else scan(dan_gdnc::chunk_scan_kernel<__bf16, LW, LC>, LW, LC);
   } else {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<_Float16>, dim3((unsigned)prep), block, 0, s, p);
-    if (shortrun) hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<_Float16, dan_gdnc::kScanShortWaves>), dim3((unsigned)scan), sblock, 0, s, p);
-    else hipLaunchKernelGGL((dan_gdnc::chunk_scan_kernel<_Float16, dan_gdnc::kScanLongWaves>), dim3((unsigned)scan), sblock, 0, s, p);
+    if (shortrun) scan(dan_gdnc::chunk_scan_kernel<_Float16, SW, SC>, SW, SC);
+    else scan(dan_gdnc::chunk_scan_kernel<_Float16, LW, LC>, LW, LC);
   }
   return hipGetLastError();
 }

@@ -76,9 +76,10 @@ def test_split_run_is_bit_identical(gpu):
 
 @pytest.mark.parametrize("lengths", [[600, 1, 0, 700, 65], [40, 3, 64, 100, 17, 1]])
 def test_chunk_form_scan_variants(gpu, lengths):
-    """Calls whose runs average more than 256 tokens take the 8-wave scan,
-    others the 4-wave one (DAN_GDN_SHORT_RUN); both against the recurrence,
-    with ragged and empty runs and GQA."""
+    """Calls whose runs average more than 256 tokens take the long-run scan
+    (16 state columns per work group), others the short-run one (32 columns;
+    DAN_GDN_SHORT_RUN); both against the recurrence, with ragged and empty
+    runs and GQA."""
     say(f"delta rule, chunked form: runs {lengths} (mean {sum(lengths) / len(lengths):.0f})")
     q, k, v, g, b, st = inputs(lengths, 1, 2, 128, torch.bfloat16, gpu, seed=11)
     out, fin = delta_rule(q, k, v, g, b, lengths, st, form="chunk")
@@ -88,10 +89,11 @@ def test_chunk_form_scan_variants(gpu, lengths):
 
 
 def test_chunk_scan_variants_bit_identical(gpu):
-    """Two runs of 300 tokens average 300 (the 8-wave scan); with two empty
-    runs appended they average 150 (the 4-wave scan). Both builds add the same
-    products in the same order, so outputs and final states are bit-identical."""
-    say("delta rule, chunked form: 8-wave vs 4-wave scan on the same runs")
+    """Two runs of 300 tokens average 300 (the long-run scan, 16 columns per
+    work group); with two empty runs appended they average 150 (the short-run
+    scan, 32 columns). Both builds add the same products in the same order,
+    so outputs and final states are bit-identical."""
+    say("delta rule, chunked form: long-run vs short-run scan on the same runs")
     q, k, v, g, b, st = inputs([300, 300], 2, 2, 128, torch.bfloat16, gpu, seed=5)
     o8, f8 = delta_rule(q, k, v, g, b, [300, 300], st, form="chunk")
     st4 = torch.cat([st, torch.zeros_like(st)])
