@@ -17,7 +17,8 @@
 //   - A unit is one work item (a tile of query tokens of one segment) for one
 //     head group (kv head + Hkv * chunk). A work group (8 waves, 2 per SIMD)
 //     runs units one after another. Wave w takes query head (w % hpw) of the
-//     kv group and the (w / hpw)-th run of 32 tokens, so the K / V^T tiles
+//     kv group and the (w / hpw)-th run of 32 tokens (16 at head_dim 256,
+//     on 16x16 products with two stage buffers), so the K / V^T tiles
 //     staged in LDS serve every query head that shares them (GQA head
 //     packing).
 //   - The grid is persistent: about one work group per CU, each walking a
@@ -64,26 +65,30 @@
 namespace dan {
 
 constexpr int kKeyTile = DAN_TREE_ATTN_KEY_TILE;  // keys per tile
-constexpr int kWaveQ = 32;                        // queries per wave
-// Work-group shape of the attention launch by head_dim: 8 waves (2 per SIMD)
-// up to D = 128; 4 waves (1 per SIMD, each with 512 registers, O^T in
-// accumulation registers) at D = 256, whose O^T (128 registers) and Q
-// fragments (64) do not fit a wave's 256 registers next to two S tiles.
+// Work-group shape of the attention launch: 8 waves, 2 per SIMD. A wave
+// takes 32 queries on 32x32 products up to D = 128, and 16 queries on 16x16
+// products at D = 256, where 32 queries' O^T (128 registers) and Q
+// fragments (64) would not fit a wave's 256 registers next to the scores.
 template <int D>
 struct Shape {
-  static constexpr int waves = D == 256 ? 4 : 8;
+  static constexpr int waves = 8;
   static constexpr int threads = 64 * waves;
-  static constexpr int waves_per_simd = D == 256 ? 1 : 2;
+  static constexpr int waves_per_simd = 2;
+  static constexpr int wave_q = D == 256 ? 16 : 32;  // queries per wave
 };
-inline int waves_for(int head_dim) { return head_dim == 256 ? Shape<256>::waves : Shape<128>::waves; }
-// Waves 0..kIssuers-1 (one per SIMD) issue every direct load of the stage
-// buffers; their SIMD partners only compute. The loads queue at the CU's
-// address unit; a queued wave cannot issue anything else, so the stall is
-// given to the wave that has slack (the older wave of each SIMD wins issue
+inline int wave_q_for(int head_dim) { return head_dim == 256 ? Shape<256>::wave_q : Shape<128>::wave_q; }
+// Up to head_dim 128, waves 0-3 (one per SIMD) issue every direct load of
+// the stage buffers; their SIMD partners only compute. The loads queue at the
+// CU's address unit; a queued wave cannot issue anything else, so the stall
+// is given to the wave that has slack (the older wave of each SIMD wins issue
 // arbitration and otherwise waits at the step barrier), and its partner runs
 // its S products alone meanwhile: the two waves of a SIMD settle half a phase
-// apart.
-constexpr int kIssuers = 4;
+// apart. At head_dim 256 the tiles are twice as large and all eight waves
+// issue (8 loads of 1 KB per issuing wave and tile either way).
+template <int D>
+struct Issuers {
+  static constexpr int n = D == 256 ? 8 : 4;
+};
 constexpr float kLog2Limit = 15.0f;  // p = exp2(S c - m) <= 2^15: P stays inside fp16's range
 constexpr int kVoteBytes = 16;       // LDS past the stage ring: the work group's overflow votes
 
@@ -365,10 +370,48 @@ __device__ inline float dot_frag<E4M3>(const Frag<E4M3> &a, const Frag<E4M3> &b,
   return acc;
 }
 
-// LDS row of key `r` (0..63) in the K tile: bits 2 and 3 swapped, which makes
-// the S^T accumulator of lane l, register i hold key 16*(i/8) + 8*(l/32) + i%8
-// of its 32-key block -- exactly the k-order of the P^T B operand.
-__device__ inline int k_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+// 16x16 products (head_dim 256, 16 queries per wave): A is 16 rows x one
+// k-step, B one k-step x 16 columns, lane l holding row / column l % 16 and
+// the k-range part l / 16 of the step; the accumulator of lane l holds rows
+// 4 (l / 16) .. + 3 of column l % 16.
+template <typename TC>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ inline f32x4 mfma16<__bf16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f32x4 mfma16<_Float16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <typename T>
+__device__ inline f32x4 mfma16_qk(const Frag<T> &a, const Frag<T> &b, f32x4 c) {
+  return mfma16<T>(a.c[0], b.c[0], c);
+}
+template <>
+__device__ inline f32x4 mfma16_qk<E4M3>(const Frag<E4M3> &a, const Frag<E4M3> &b, f32x4 c) {
+  const i32x8 x = __builtin_bit_cast(i32x8, a), y = __builtin_bit_cast(i32x8, b);
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, c, 0, 0, 0, 0, 0, 0);  // OCP e4m3 x e4m3, no block scales
+}
+
+// Key held in LDS row r of a K tile (0..63), head_dim 256: within each 32-row
+// group, row 16 h + 4 q + e holds key 8 q + 4 h + e. The 16x16 product of
+// row block 2 g + h then gives lane l (q = l / 16) keys 32 g + 8 q + 4 h + e,
+// so across blocks 2 g and 2 g + 1 a lane holds keys 32 g + 8 q .. + 7 of its
+// query: exactly its part of the P^T B operand of the next product.
+__host__ __device__ constexpr int k_row16(int r) {
+  return (r & ~31) | (((r >> 2) & 3) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
+}
+
+// Key held in LDS row r of a K tile (0..63), head_dim <= 128: bits 2 and 3
+// swapped, which makes the S^T accumulator of lane l, register i hold key
+// 16*(i/8) + 8*(l/32) + i%8 of its 32-key block -- exactly the k-order of
+// the P^T B operand.
+template <int D>
+__device__ inline int k_row(int r) {
+  if constexpr (D == 256) return k_row16(r);
+  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
 
 
 // The value of lane l and of lane l ^ 32 (v_permlane32_swap on a copy). The
@@ -467,6 +510,7 @@ struct Lds {
   static constexpr int vBytes = D * kKeyTile * 2;         // fp16 V^T tile
   static constexpr int vBlocks = vBytes / 1024;
   static constexpr int blocks = kBlocks + vBlocks;
+  static constexpr int kIssuers = Issuers<D>::n;
   static_assert(kBlocks % kIssuers == 0 && vBlocks % kIssuers == 0, "blocks divide evenly among the issuing waves");
   static constexpr int slots = blocks / kIssuers;  // direct loads per issuing wave per tile
   static constexpr int buf = kBytes + vBytes;
@@ -645,7 +689,9 @@ void tree_attn_kernel(const KParams args) {
   // Two stage buffers (head_dim 256): one wave per SIMD, every wave issues,
   // and each step processes one tile while the next one loads.
   constexpr bool kTwoStage = NB == 2;
-  static_assert(NB == 4 || (NB == 2 && Shape<D>::waves == kIssuers), "ring of 4, or 2 with every wave issuing");
+  static_assert(NB == 4 || (NB == 2 && D == 256), "ring of 4, or 2 at head_dim 256");
+  constexpr int WQ = Shape<D>::wave_q;  // queries per wave
+  constexpr int kIssuers = Issuers<D>::n;  // waves that issue the stage loads
   constexpr bool kF8 = std::is_same<TQK, E4M3>::value;
   constexpr int KS = QK<TQK>::step;                   // k-step of Q K^T
   constexpr int NK = D / KS;                          // k-steps of Q K^T
@@ -661,6 +707,9 @@ void tree_attn_kernel(const KParams args) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, hl = lane >> 5, lq = lane & 31;
+  // The lane's query within the wave, and which part of a k-step of S it
+  // holds (32x32 products: two halves; 16x16: four quarters).
+  const int lqq = WQ == 16 ? (lane & 15) : lq, kpart = WQ == 16 ? (lane >> 4) : hl;
   // LDS byte offsets of this lane's operand reads (see Lds). K: row lq of a
   // 32-row block with its chunk swizzle and half-step folded in; the chunk
   // of each k-step is XOR'd in per read (it only touches the low bits).
@@ -728,7 +777,7 @@ void tree_attn_kernel(const KParams args) {
   auto k_offset = [&](int blk, int64_t st) __attribute__((always_inline)) {  // bytes
     const int pos = blk * 64 + lane, m = pos / NC;
     const int c = (pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m);
-    return (uint32_t)((k_row(m) * st + c * CE) * (int64_t)sizeof(TQK));
+    return (uint32_t)((k_row<D>(m) * st + c * CE) * (int64_t)sizeof(TQK));
   };
   uint32_t off_a[SLOTS];  // K: new-token offsets; V^T: offsets in the copy
   {
@@ -775,7 +824,7 @@ void tree_attn_kernel(const KParams args) {
       for (int sl = 0; sl < SK; ++sl) {
         const int pos = (wave + kIssuers * sl) * 64 + lane, m = pos / NC;
         const int col = CE * ((pos % NC) ^ kswz<D, (int)sizeof(TQK)>(m));
-        const int key = min(kb + k_row(m), PN - 1);
+        const int key = min(kb + k_row<D>(m), PN - 1);
         dma16(key < P ? pkp + (int64_t)key * pk_st + col : kp + (int64_t)(start + key - P) * k_st + col,
               dst + (uint32_t)(sl * kIssuers * 1024));
       }
@@ -814,15 +863,17 @@ void tree_attn_kernel(const KParams args) {
   auto load_q = [&](const KParams &p, const DanUnit &un) __attribute__((always_inline)) {
     const int g = un.group, kvh = g % p.num_kv_heads, chunk = g / p.num_kv_heads;
     const int hig = chunk * p.hpw + (wave % p.hpw), head = kvh * p.rep + hig;
-    const int qw0 = un.item.t0 + (wave / p.hpw) * kWaveQ, qend = un.item.t0 + un.item.tq;
-    const int ql = qw0 + lq;
+    const int qw0 = un.item.t0 + (wave / p.hpw) * WQ, qend = un.item.t0 + un.item.tq;
+    const int ql = qw0 + lqq;
     const bool qvalid = hig < p.rep && qw0 < qend && ql < qend;
     const int qrow = un.start + min(ql, qend - 1);
     qlo = qvalid ? *gbl(p.key_lo + qrow) : 0;
     const TQK *row = static_cast<const TQK *>(p.q) + (int64_t)qrow * p.q_st +
-                     (int64_t)min(head, p.num_kv_heads * p.rep - 1) * p.q_sh + KS / 2 * hl;
+                     (int64_t)min(head, p.num_kv_heads * p.rep - 1) * p.q_sh + KS / 2 * kpart;
+    // 16x16 products take k-steps twice as long as the 32x32 ones
+    constexpr int QS = WQ == 16 ? 2 * KS : KS;
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) qf[kk] = load_frag<TQK>(row + KS * kk);
+    for (int kk = 0; kk < D / QS; ++kk) qf[kk] = load_frag<TQK>(row + QS * kk);
   };
   for (int u = u_begin; u < u_end; ++u) {
     KArgPtr kp_u = kseg;
@@ -865,7 +916,7 @@ void tree_attn_kernel(const KParams args) {
 
     const int hig = chunk * p.hpw + (wave % p.hpw);
     const int head = kvh * p.rep + hig;
-    const int qw0 = w.t0 + (wave / p.hpw) * kWaveQ;  // wave's first query (segment-local)
+    const int qw0 = w.t0 + (wave / p.hpw) * WQ;  // wave's first query (segment-local)
     const int qend = w.t0 + w.tq;
     const bool wave_work = hig < p.rep && qw0 < qend;
 
@@ -882,7 +933,7 @@ void tree_attn_kernel(const KParams args) {
     // Per-lane query state: lane owns query column lq of its wave. Padding
     // columns (past the tile, or an idle wave) read a clamped valid row and see
     // every key, so they stay finite; they are never stored.
-    const int ql = qw0 + lq;
+    const int ql = qw0 + lqq;
     const bool qvalid = wave_work && ql < qend;
     const int qk = qvalid ? P + ql : 0x3fffffff;
 
@@ -904,33 +955,6 @@ void tree_attn_kernel(const KParams args) {
       const uint32_t kbase = (uint32_t)(uintptr_t)(DAN_LDS uint8_t *)(smem + b * L::buf) + k_lane;
       s[0] = f32x16{};
       s[1] = f32x16{};
-      if constexpr (kTwoStage) {
-        // Operand fragments are read W = 2 k-steps ahead of their products.
-        // Reading all NK first (128 VGPRs at bf16) made the compiler spill
-        // to scratch inside the tile loop; two k-steps keep the matrix core
-        // fed with no spill.
-        constexpr int W = NK < 2 ? NK : 2;
-        Frag<TQK> a[NK][2];
-        auto rd = [&](int kk) __attribute__((always_inline)) {
-#pragma unroll
-          for (int i = 0; i < CH; ++i) {
-            const uint32_t off = kbase ^ (uint32_t)((2 * kk * CH + i) * 16);
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-              a[kk][mb].c[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(off + mb * 32 * RB));
-          }
-        };
-#pragma unroll
-        for (int kk = 0; kk < W; ++kk) rd(kk);
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-          if (kk + W < NK) rd(kk + W);
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb) s[mb] = mfma_qk<TQK>(a[kk][mb], qf[kk], s[mb]);
-          after_kstep(kk);
-        }
-        return;
-      }
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         Frag<TQK> a[2];
@@ -1075,23 +1099,6 @@ void tree_attn_kernel(const KParams args) {
     // O's scale: begin_tile).
     auto pv_phase = [&](int b) __attribute__((always_inline)) {
       const uint8_t *vbuf = smem + b * L::buf + v_lane;
-      if constexpr (kTwoStage) {
-        // V^T fragments two key groups (of four) ahead of their products.
-        u32x4 a[4][ND];
-        auto rd = [&](int kj) __attribute__((always_inline)) {
-#pragma unroll
-          for (int db = 0; db < ND; ++db) a[kj][db] = *reinterpret_cast<const u32x4 *>(vbuf + (kj * ND + db) * 1024);
-        };
-        rd(0);
-        rd(1);
-#pragma unroll
-        for (int kj = 0; kj < 4; ++kj) {
-          if (kj + 2 < 4) rd(kj + 2);
-#pragma unroll
-          for (int db = 0; db < ND; ++db) o[db] = mfma32<_Float16>(a[kj][db], pf[kj], o[db]);
-        }
-        return;
-      }
 #pragma unroll
       for (int kj = 0; kj < 4; ++kj) {
 #pragma unroll
@@ -1105,21 +1112,164 @@ void tree_attn_kernel(const KParams args) {
     auto tile_of = [&](int i) __attribute__((always_inline)) { return i < w.ja1 ? i : w.jb0 + (i - w.ja1); };
 
     if constexpr (kTwoStage) {
-      // Two stage buffers: each step waits for its tile, passes the barrier
-      // (after which the other buffer, last used by the previous step, is
-      // free), issues the next tile there and processes its own: S, mask,
-      // softmax, then O += V P. The running max starts at the first tile's
-      // largest visible score, as below.
-      issue(cur, off_b, 0, gbase & (NB - 1));
+      // head_dim 256: 16 queries per wave on 16x16 products, two waves per
+      // SIMD, two stage buffers. Each step waits for its tile, passes the
+      // barrier (after which the other buffer, last used by the previous step,
+      // is free), the issuing waves load the next tile there, and every wave
+      // processes its own: S, mask, softmax, then O += V P. The running max
+      // starts at the first tile's largest visible score and is raised per
+      // tile when a score would put p above 2^kLog2Limit.
+      static_assert(L::kRowsPerPeriod == 1 && L::kSwizzle == 16, "the K row swizzle of the 16x16 reads");
+      constexpr int NK2 = D / (2 * KS);   // k-steps of S (16x16 products)
+      constexpr int CPK = 2 * KS / CE;    // 16-byte chunks per k-step and row
+      constexpr int NDB = D / 16;         // 16-row d blocks of O^T
+      const int q4 = lane >> 4, l16 = lane & 15;
+      f32x4 o4[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o4[db] = f32x4{};
+      u32x4 pf2[2];  // P^T of the tile (fp16): keys 32 g + 8 q4 .. + 7
+      // S^T = K Q^T: block bb of 16 keys (LDS rows 16 bb .. + 15), lane row
+      // 16 bb + l16 whose swizzle is l16, k-step kk's chunks kk CPK + q4 CH + i.
+      auto qk16 = [&](int b, f32x4(&s)[4], auto &&after_kstep) __attribute__((always_inline)) {
+        const uint32_t base = smem_lds + (uint32_t)(b * L::buf + l16 * RB);
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) s[bb] = f32x4{};
+        constexpr int W = 1;  // k-steps of operand fragments read ahead
+        Frag<TQK> a[NK2][4];
+        auto rd = [&](int kk) __attribute__((always_inline)) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            const uint32_t off = base + (uint32_t)(((kk * CPK + q4 * CH + i) ^ l16) * 16);
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+              a[kk][bb].c[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(off + bb * 16 * RB));
+          }
+        };
+#pragma unroll
+        for (int kk = 0; kk < W; ++kk) rd(kk);
+#pragma unroll
+        for (int kk = 0; kk < NK2; ++kk) {
+          if (kk + W < NK2) rd(kk + W);
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) s[bb] = mfma16_qk<TQK>(a[kk][bb], qf[kk], s[bb]);
+          after_kstep(kk);
+        }
+      };
+      // key (within the tile) of register e of block bb in this lane
+      auto rel16 = [&](int bb, int e) __attribute__((always_inline)) { return 32 * (bb >> 1) + 8 * q4 + 4 * (bb & 1) + e; };
+      auto mask16 = [&](int j, f32x4(&s)[4]) __attribute__((always_inline)) {
+        if (j < w.jfull) return;
+        const int kb = j * kKeyTile;
+        const int lim = qk - kb;  // visible: rel <= lim
+        if (kb + kKeyTile > PT && kb < w.lo_max) {
+          const int g0 = PT - kb, g1 = qlo - kb;  // hidden: g0 <= rel < g1
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int rel = rel16(bb, e);
+              s[bb][e] = rel <= lim && (rel < g0 || rel >= g1) ? s[bb][e] : -INFINITY;
+            }
+        } else {
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[bb][e] = rel16(bb, e) <= lim ? s[bb][e] : -INFINITY;
+        }
+      };
+      auto fix16 = [&](int j, f32x4(&s)[4]) __attribute__((always_inline)) {
+        const int kb = j * kKeyTile;
+        if (c_past == c_new || !(kb < P && kb + kKeyTile > P)) return;
+        const float ratio = c_past / c_new;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[bb][e] = rel16(bb, e) < P - kb ? s[bb][e] * ratio : s[bb][e];
+      };
+      // the lane's largest score (16), and its query's (the lanes l16 + 16 q)
+      auto lmax16 = [&](const f32x4(&s)[4]) __attribute__((always_inline)) {
+        auto max3 = [](float a, float b, float c) __attribute__((always_inline)) { return fmaxf(fmaxf(a, b), c); };
+        const float a0 = max3(s[0][0], s[0][1], s[0][2]), a1 = max3(s[0][3], s[1][0], s[1][1]);
+        const float a2 = max3(s[1][2], s[1][3], s[2][0]), a3 = max3(s[2][1], s[2][2], s[2][3]);
+        const float a4 = max3(s[3][0], s[3][1], s[3][2]);
+        return fmaxf(max3(a0, a1, a2), max3(a3, a4, s[3][3]));
+      };
+      auto qmax16 = [&](const f32x4(&s)[4]) __attribute__((always_inline)) {
+        float m = lmax16(s);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        return fmaxf(m, __shfl_xor(m, 32));
+      };
+      auto begin16 = [&](const f32x4(&s)[4], float c, int ve) __attribute__((always_inline)) {
+        const bool raise = __any(!(fmaf(lmax16(s), c, mneg) <= kLog2Limit));
+        if (raise || ve != vE) {
+          float f = exp2i(vE - ve);
+          if (raise) {
+            const float mold = -mneg;
+            const float mnew = fmaxf(mold, qmax16(s) * c);
+            const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+            mneg = -mnew;
+            lsum *= alpha;
+            f *= alpha;
+          }
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) o4[db] *= f;
+          vE = ve;
+        }
+      };
+      auto exp16 = [&](const f32x4(&s)[4], float c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          f32x8 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[e] = __builtin_amdgcn_exp2f(fmaf(s[2 * g][e], c, mneg));
+            x[4 + e] = __builtin_amdgcn_exp2f(fmaf(s[2 * g + 1][e], c, mneg));
+          }
+          pf2[g] = pack8<_Float16>(x);
+        }
+        float acc[2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const f16x8 h = __builtin_bit_cast(f16x8, pf2[g]);
+          acc[g] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 0, 1), kOnes2, 0.f, false);
+          acc[g] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 2, 3), kOnes2, acc[g], false);
+          acc[g] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 4, 5), kOnes2, acc[g], false);
+          acc[g] = __builtin_amdgcn_fdot2(__builtin_shufflevector(h, h, 6, 7), kOnes2, acc[g], false);
+        }
+        return acc[0] + acc[1];
+      };
+      // O^T += V^T P^T: the A fragment of d block dbb (16 rows) and key group g
+      // (32 keys) is read from the copy's 32x32 fragments: lane (l16, q4)
+      // holds d 16 dbb + l16, keys 32 g + 8 q4 .. + 7, which is lane
+      // 32 (q4 % 2) + 16 (dbb % 2) + l16 of fragment (key group 2 g + q4 / 2,
+      // d block dbb / 2).
+      const uint32_t vlane16 = (uint32_t)(L::kBytes + (q4 >> 1) * ND * 1024 + (32 * (q4 & 1) + l16) * 16);
+      auto pv16 = [&](int b) __attribute__((always_inline)) {
+        const uint32_t vb = smem_lds + (uint32_t)(b * L::buf) + vlane16;
+        constexpr int NV = 2 * NDB, WV = 2;
+        u32x4 a[NV];
+        auto rd = [&](int i) __attribute__((always_inline)) {
+          const int g = i / NDB, db = i % NDB;
+          a[i] = *reinterpret_cast<const DAN_LDS u32x4 *>((uintptr_t)(vb + (uint32_t)((2 * g * ND + db / 2) * 1024 + (db & 1) * 256)));
+        };
+#pragma unroll
+        for (int i = 0; i < WV; ++i) rd(i);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          if (i + WV < NV) rd(i + WV);
+          o4[i % NDB] = mfma16<_Float16>(a[i], pf2[i / NDB], o4[i % NDB]);
+        }
+      };
+
+      if (wave < kIssuers) issue(cur, off_b, 0, gbase & (NB - 1));
       load_q(p, un);
-      f32x16 s[2];
+      f32x4 s[4];
       for (int it = 0; it < ntile; ++it) {
         wait_vmem<0>();
         barrier_lds();
         const int ve = load_scalar(vexp_u + tile_of(it));
-        // The next tile's loads go out one slot per k-step of this tile's S
-        // (a wave alone on its SIMD would otherwise stall on the burst); a
-        // tile straddling the past/new boundary issues them all now.
+        // The next tile's loads go out over this tile's S products (two per
+        // k-step); a tile straddling the past/new boundary issues them all now.
         int kind = 2;
         const TQK *sp_tb = cur.kp;
         const _Float16 *sp_vtt = cur.vtp;
@@ -1130,26 +1280,36 @@ void tree_attn_kernel(const KParams args) {
           sp_tb = kind == 0 ? cur.pkp + (int64_t)kb * cur.pk_st : cur.kp + (int64_t)(cur.start + kb - P) * cur.k_st;
           sp_vtt = cur.vtp + (int64_t)j * (D * kKeyTile);
           sp_dst = smem_lds + (uint32_t)(((gbase + i) & (NB - 1)) * L::buf + wave * 1024);
-          if (kind == 2) issue(cur, off_b, i, (gbase + i) & (NB - 1));
+          if (kind == 2 && wave < kIssuers) issue(cur, off_b, i, (gbase + i) & (NB - 1));
         }
-        if (kind != 2) {
-          qk_phase((gbase + it) & (NB - 1), s, [&](int kk) __attribute__((always_inline)) {
+        if (kind != 2 && wave < kIssuers) {
+          qk16((gbase + it) & (NB - 1), s, [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
-            for (int sl = kk * SLOTS / NK; sl < (kk + 1) * SLOTS / NK; ++sl) {
+            for (int sl = kk * SLOTS / NK2; sl < (kk + 1) * SLOTS / NK2; ++sl) {
               if (sl < SK) dma16(sp_tb, kind == 0 ? off_b[sl] : off_a[sl], sp_dst + (uint32_t)(sl * kIssuers * 1024));
               else dma16(sp_vtt, off_a[sl], sp_dst + (uint32_t)(sl * kIssuers * 1024));
             }
           });
         } else {
-          qk_phase((gbase + it) & (NB - 1), s, [](int) {});
+          qk16((gbase + it) & (NB - 1), s, [](int) {});
         }
-        mask_phase(tile_of(it), s);
-        fix_straddle(tile_of(it), s);
+        mask16(tile_of(it), s);
+        fix16(tile_of(it), s);
         const float c = tile_c(tile_of(it));
-        if (it == 0) mneg = -fmaxf(s_max(s) * c, -3.0e38f);
-        begin_tile(true, s, c, ve);
-        lsum += exp_phase(s, c);
-        pv_phase((gbase + it) & (NB - 1));
+        if (it == 0) mneg = -fmaxf(qmax16(s) * c, -3.0e38f);
+        begin16(s, c, ve);
+        lsum += exp16(s, c);
+        pv16((gbase + it) & (NB - 1));
+      }
+      // Epilogue: O = O^T / l, the query's l summed over its four lanes.
+      // Lane (l16, q4) holds d 16 db + 4 q4 .. + 3 of block db.
+      float l = lsum + __shfl_xor(lsum, 16);
+      l += __shfl_xor(l, 32);
+      const float linv = l > 0.f ? exp2i(vE) / l : 0.f;
+      TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(cur.start + ql) * p.o_st + (int64_t)head * p.o_sh;
+      if (qvalid) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) store4<TOut>(orow + 16 * db + 4 * q4, o4[db] * linv);
       }
       nn = 0;
     } else {
@@ -1254,29 +1414,31 @@ void tree_attn_kernel(const KParams args) {
       }
     }
 
-    // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
-    // r4 of block db holds d = 32 db + 8 r4 + 4 hl + (0..3); lanes l and
-    // l ^ 32 (the same query) trade halves so that each stores 8 contiguous
-    // d: lane hl = 0 the even groups, hl = 1 the odd ones.
-    const float l = lsum + __shfl_xor(lsum, 32);
-    const float linv = l > 0.f ? exp2i(vE) / l : 0.f;
-    TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(cur.start + ql) * p.o_st + (int64_t)head * p.o_sh;
-#pragma unroll
-    for (int db = 0; db < ND; ++db)
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        const Out4<TOut> e = pack_out<TOut>(o[db], 8 * jp, linv), od = pack_out<TOut>(o[db], 8 * jp + 4, linv);
-        // v_permlane32_swap(e, od) leaves lanes below 32 (e, partner's e) and lanes from 32
-        // (partner's od, od): each lane's 8 contiguous d in order, with no select.
-        Out4<TOut> first, second;
-#pragma unroll
-        for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(e.w[w4], od.w[w4], false, false);
-          first.w[w4] = sw[0];
-          second.w[w4] = sw[1];
+    if constexpr (!kTwoStage) {
+      // Epilogue: O = O^T / l, written token-major [N, H, D]. Register group
+      // r4 of block db holds d = 32 db + 8 r4 + 4 hl + (0..3); lanes l and
+      // l ^ 32 (the same query) trade halves so that each stores 8 contiguous
+      // d: lane hl = 0 the even groups, hl = 1 the odd ones.
+      const float l = lsum + __shfl_xor(lsum, 32);
+      const float linv = l > 0.f ? exp2i(vE) / l : 0.f;
+      TOut *orow = static_cast<TOut *>(p.o) + (int64_t)(cur.start + ql) * p.o_st + (int64_t)head * p.o_sh;
+  #pragma unroll
+      for (int db = 0; db < ND; ++db)
+  #pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const Out4<TOut> e = pack_out<TOut>(o[db], 8 * jp, linv), od = pack_out<TOut>(o[db], 8 * jp + 4, linv);
+          // v_permlane32_swap(e, od) leaves lanes below 32 (e, partner's e) and lanes from 32
+          // (partner's od, od): each lane's 8 contiguous d in order, with no select.
+          Out4<TOut> first, second;
+  #pragma unroll
+          for (int w4 = 0; w4 < Out4<TOut>::kWords; ++w4) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(e.w[w4], od.w[w4], false, false);
+            first.w[w4] = sw[0];
+            second.w[w4] = sw[1];
+          }
+          if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), first, second);
         }
-        if (qvalid) store8<TOut>(orow + 32 * db + 8 * (2 * jp + hl), first, second);
-      }
+    }
     gbase += ntile;
     pre = nn;
   }  // units
@@ -1432,7 +1594,7 @@ const char *dan_tree_attn_last_error(void) { return dan::g_err; }
 int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
-  return dan::kWaveQ * dan::waves_for(head_dim) / dan::heads_per_group(num_heads / num_kv_heads);
+  return dan::wave_q_for(head_dim) * dan::Shape<128>::waves / dan::heads_per_group(num_heads / num_kv_heads);
 }
 
 int dan_tree_attn_head_groups(int32_t num_heads, int32_t num_kv_heads) {

@@ -253,8 +253,8 @@ int dan_tree_attn_fwd_noalloc(const DanTreeAttnArgs *args, void *stream);
 
 /* Queries per work item the kernel expects for this head configuration
  * (the tile planner's counterpart of ReadLayout, dan/attention.py:155-172):
- * 32 tokens per wave times the waves per query head of a work group (8
- * waves up to head_dim 128, 4 at 256). Returns 0 for an unsupported
+ * the tokens per wave (32 up to head_dim 128, 16 at 256) times the waves
+ * per query head of a work group of 8 waves. Returns 0 for an unsupported
  * configuration. */
 int dan_tree_attn_tile_q(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim);
 
