@@ -2,8 +2,9 @@
 attend (dan/models/qwen3_5.py:327) with 16 q / 2 kv heads of 256 after a
 zero-centered q/k RMSNorm and a partial rotary embedding.
 
-The kernel runs these with one wave per SIMD and two stage buffers (a
-64 KB K + V^T tile pair per buffer). Same bars as the other parity tests:
+The kernel runs these with 16 queries per wave on 16x16 products, two
+waves per SIMD, and two stage buffers (a 64 KB K + V^T tile pair per
+buffer). Same bars as the other parity tests:
 max-abs 2e-2 against the fp32 oracle, readout 1e-3 (e4m3: against the
 oracle on the dequantized inputs)."""
 import numpy as np
