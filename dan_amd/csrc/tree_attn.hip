@@ -686,8 +686,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(Shape<D>::threads, Shape<D
 void tree_attn_kernel(const KParams args) {
   using L = Lds<D, (int)sizeof(TQK)>;
   constexpr int NB = L::nbuf;
-  // Two stage buffers (head_dim 256): one wave per SIMD, every wave issues,
-  // and each step processes one tile while the next one loads.
+  // Two stage buffers (head_dim 256): 16 queries per wave on 16x16 products,
+  // every wave issues, and each step processes one tile while the next one
+  // loads.
   constexpr bool kTwoStage = NB == 2;
   static_assert(NB == 4 || (NB == 2 && D == 256), "ring of 4, or 2 at head_dim 256");
   constexpr int WQ = Shape<D>::wave_q;  // queries per wave

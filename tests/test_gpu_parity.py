@@ -141,31 +141,36 @@ def _scored_batch(gpu, structure, score_fn, h=8, hkv=2, d=128, seed=0):
     return W.Workload("scored", to(q), to(k), to(v), segs, 0, {})
 
 
-def test_running_max_set_by_first_visible_key(gpu):
+# head_dim 256 runs its own step (16 queries per wave, 16x16 products) with its
+# own running-max start and per-tile raise: the score-shaped cases run there too.
+@pytest.mark.parametrize("d", [128, 256])
+def test_running_max_set_by_first_visible_key(gpu, d):
     """Empty trunk, two branches; the second branch's queries share a work
     item with the first branch's tail but see none of key tile 0. All scores
     are near -300 / sqrt(D) * log2 e below zero, so a running max left at 0
     would underflow every probability."""
     w = _scored_batch(gpu, [(0, [80, 70])], lambda t: (np.full(t.shape, -20.0, np.float32),
-                                                          np.full(t.shape, 15.0, np.float32) + 0.01 * t))
-    check(w, "negative scores, first visible key after tile 0")
+                                                          np.full(t.shape, 15.0, np.float32) + 0.01 * t), d=d)
+    check(w, f"negative scores, first visible key after tile 0, D={d}")
 
 
-def test_running_max_raised_by_growing_scores(gpu):
+@pytest.mark.parametrize("d", [128, 256])
+def test_running_max_raised_by_growing_scores(gpu, d):
     """Scores grow with the key index along a 1000-token trunk, so later
     tiles keep exceeding the running max: the rescale path runs on most
     tiles."""
     w = _scored_batch(gpu, [(1000, [40, 24])], lambda t: (np.full(t.shape, 4.0, np.float32),
-                                                          0.1 * t.astype(np.float32)))
-    check(w, "growing scores")
+                                                          0.1 * t.astype(np.float32)), d=d)
+    check(w, f"growing scores, D={d}")
 
 
 def _as_dtype(w, dtype):
     return W.Workload(f"{w.name}-{dtype}", w.q.to(dtype), w.k.to(dtype), w.v.to(dtype), w.segments, w.layer, {})
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("dtype", ["fp32", "bf16", "e4m3"])
-def test_overflowing_units_among_others(gpu, dtype):
+def test_overflowing_units_among_others(gpu, dtype, d):
     """The kernel runs a unit without the per-tile overflow check and runs it
     again with the check when a probability overflowed fp16. Here the first
     segment's scores grow along its 600-token trunk (its units overflow and
@@ -178,26 +183,27 @@ def test_overflowing_units_among_others(gpu, dtype):
     def scores(t):
         b = np.where(t < first, 0.1 * t, 0.5).astype(np.float32)
         return np.full(t.shape, 4.0, np.float32), b
-    w = _scored_batch(gpu, structure, scores)
+    w = _scored_batch(gpu, structure, scores, d=d)
     if dtype == "e4m3":
-        _fp8_case(w, "overflowing units among others (e4m3)", gpu, vs_original=False)
+        _fp8_case(w, f"overflowing units among others (e4m3, D={d})", gpu, vs_original=False)
         return
-    check(w if dtype == "fp32" else _as_dtype(w, torch.bfloat16), f"overflowing units among others ({dtype})")
+    check(w if dtype == "fp32" else _as_dtype(w, torch.bfloat16), f"overflowing units among others ({dtype}, D={d})")
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("rise", [15.5, 16.5])
-def test_probabilities_near_fp16_limit(gpu, rise):
+def test_probabilities_near_fp16_limit(gpu, rise, d):
     """Keys 0-63 score 0 and every later key scores `rise` (log2 units) above
     them, so queries past the first tile start from m = 0 and then meet
     p = 2^rise: 2^15.5 fits fp16 (one pass, P up to 46341), 2^16.5 overflows
-    it (the unit runs again with the check, which raises m)."""
-    d = 128
+    it (at head_dim <= 128 the unit runs again with the check, which raises m;
+    at 256 the per-tile check raises m on the tile)."""
     raw = rise / (math.log2(math.e) / math.sqrt(d))  # raw q.k giving S * scale * log2(e) = rise
 
     def scores(t):
         return np.full(t.shape, 4.0, np.float32), np.where(t < 64, 0.0, raw / 4.0).astype(np.float32)
     w = _scored_batch(gpu, [(300, [40, 24])], scores, d=d)
-    check(w, f"probabilities near the fp16 limit (rise {rise})")
+    check(w, f"probabilities near the fp16 limit (rise {rise}, D={d})")
 
 
 def dequantized(w):
