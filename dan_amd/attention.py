@@ -328,8 +328,17 @@ def _attend_fused(q, k, v, segments, layer, scale, fp8_scales=None, phases=_nati
         raise ValueError("noalloc calls run both phases (PHASES_ALL); a split call needs a workspace")
     if phases != _native.PHASES_ALL and workspace is None:
         raise ValueError("a split call (PHASE_PACK / PHASE_ATTEND) needs the workspace the two phases share")
-    return torch.ops.dan_amd.tree_attn(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc),
-                                       workspace)
+    return _call_op(*_op_args(q, k, v, segments, layer, scale, fp8_scales, phases, noalloc), workspace)
+
+
+def _call_op(*args):
+    """``torch.ops.dan_amd.tree_attn`` under ``torch.compile``; in eager mode
+    the launch itself, without the operator dispatch (the autograd and
+    in-place wrappers cost about as much host time per call as the launch:
+    the call is forward-only and its workspace is the call's own)."""
+    if torch.compiler.is_compiling():
+        return torch.ops.dan_amd.tree_attn(*args)
+    return _launch_tree_attn(*args)
 
 
 def workspace_bytes(q, k, segments):
@@ -406,6 +415,11 @@ def tree_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tables: List[to
     written by the copy, read by the attention launch), else to a block of
     torch's caching allocator on the current stream (stream-ordered reuse);
     with ``noalloc`` the library's own scratch is used instead."""
+    return _launch_tree_attn(q, k, v, tables, scales, meta, scale, workspace)
+
+
+def _launch_tree_attn(q, k, v, tables, scales, meta, scale, workspace):
+    """The body of ``tree_attn``."""
     lib = _native.load()
     h, n, d = q.shape
     hkv = k.shape[0]
@@ -621,4 +635,4 @@ class BudgetPlan:
         meta = [self.max_segments, self.max_segments, self.max_work, self.tile_q, self.max_cols * _native.KEY_TILE,
                 self.slots, _native.PHASES_ALL, 0]
         softmax_scale = (1.0 / math.sqrt(self.d)) if scale is None else float(scale)
-        return torch.ops.dan_amd.tree_attn(q, k, v, tables, scales, meta, softmax_scale, None)
+        return _call_op(q, k, v, tables, scales, meta, softmax_scale, None)
