@@ -243,8 +243,8 @@ def _stage_f16(x):
     (``dan_tree_attn_stage_f16``, two launches on the current stream)."""
     x = _kernel_view(x)
     out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
-    scale = torch.empty(1, dtype=torch.float32, device=x.device)
-    partial = torch.empty(_native.STAGE_PARTIALS, dtype=torch.float32, device=x.device)
+    scratch = torch.empty(1 + _native.STAGE_PARTIALS, dtype=torch.float32, device=x.device)  # scale, then the partials
+    scale, partial = scratch[:1], scratch[1:]
     a = _native.DanStageF16Args()
     a.abi_version = _native.ABI_VERSION
     a.d0, a.d1, a.d2 = x.shape
