@@ -431,8 +431,9 @@ def bench_gdn(args):
         "dtype": "fp32 state, bf16 io", "data": "synthetic",
         "config": {"workload": f"gdn-c3: {len(trunks)} trunks (longest {max(tl)}), {len(bl)} branches, {tokens} tokens, "
                                f"{hk}/{hv} heads, Dk = Dv = {d}", "seed": args.seed},
-        "roofline": {"bound": "fp32 MFMA, sequential in chunks of 64 tokens per run (the chunked form; a phase "
-                              "whose longest run is under deltanet.CHUNK_MIN_RUN tokens goes token by token)",
+        "roofline": {"bound": "sequential in chunks of 64 tokens per run (the chunked form; a phase whose longest "
+                              "run is under deltanet.CHUNK_MIN_RUN tokens goes token by token); fp32 arithmetic, on "
+                              "bf16 MFMA with fp32 operands as bf16 pairs for bf16 inputs; peak: the fp32 MFMA rate",
                      "achieved": round(flops / wall / 1e12, 2),
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / wall / 1e12 / 157.3, 4), "traffic": None,
                      "trunk_phase_ms": round(tr_ms, 4), "branch_phase_ms": round(br_ms, 4), "forms": forms,

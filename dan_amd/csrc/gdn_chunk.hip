@@ -19,13 +19,18 @@
 //                      v_mfma_f32_32x32x16 (exact bf16/fp16 products, fp32
 //                      sums; the norm factors and decays are applied after,
 //                      in fp32), then T by forward substitution, one column
-//                      per four lanes; T, A and the per-row factors go to the
-//                      chunk records of the workspace.
-//   chunk_scan_kernel  one work group per (run, value head, 32 state
-//                      columns), the state slice in LDS; the run's chunks in
-//                      order, each the five products above on
-//                      v_mfma_f32_16x16x4_f32 (fp32 operands: the state keeps
-//                      fp32 accuracy), q, k and v read in place.
+//                      per four lanes; T, A and the per-row factors (and for
+//                      bf16 inputs K^T) go to the chunk records of the
+//                      workspace.
+//   chunk_scan_bf16_kernel  (bf16 inputs) one work group per (run, value
+//                      head, 32 state columns), the state slice in LDS; the
+//                      run's chunks in order, each the five products above on
+//                      v_mfma_f32_16x16x32_bf16, fp32 operands as bf16 pairs
+//                      (hi + lo, ~16 significant bits) against an fp32 master
+//                      copy of the state; q, k and v read in place.
+//   chunk_scan_kernel  (fp16 inputs) the same on v_mfma_f32_16x16x4_f32 (fp32
+//                      operands), 16 state columns per work group for long
+//                      runs, 32 for many short ones.
 // The sequential critical path is one chunk step per 64 tokens.
 //
 // Chunk records: run r's chunks are slots r + cu[r] / 64 + j, j = 0, 1, ..;
@@ -34,6 +39,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "dan_gdn.h"
 
@@ -45,9 +52,19 @@ constexpr int kThreads = 256;
 // State columns per scan work group (a template argument of the scan: 32 or
 // 16) for phases of long and of short runs.
 constexpr int kLongCols = 16, kShortCols = 32;
-// Floats per (slot, value head): T [64][64], A [64][64], then five rows of 64:
-// beta gamma r_k, beta, r_q Dk^-1/2 gamma, exp(G_63 - G) r_k, {gamma_63, 0, ..}.
-constexpr int kRec = 2 * kC * kC + 5 * kC;
+// Chunk record per (slot, value head), two layouts:
+// - fp16 inputs (the fp32 scan): T [64][64] and A [64][64] in fp32, then the
+//   five rows of 64 floats below, at float kVecF32;
+// - bf16 inputs (the bf16 scan): T and A as bf16 pairs (hi = bf16(x), lo =
+//   bf16(x - hi): x to ~16 significant bits), each [64][64] row-major, then
+//   K^T [128][64] bf16 (exact), then the five rows at float kVecBf.
+// The five rows: beta gamma r_k, beta, r_q Dk^-1/2 gamma, exp(G_63 - G) r_k,
+// {gamma_63, 0, ..}.
+constexpr int kVecF32 = 2 * kC * kC;
+constexpr int kVecBf = (4 * kC * kC * 2 + kDk * kC * 2) / 4;
+constexpr int kRec = kVecBf + 5 * kC;  // floats; the fp32 layout uses the first kVecF32 + 5 * kC
+// bf16 layout: byte offsets of T hi / lo, A hi / lo and K^T.
+constexpr int kThiB = 0, kTloB = kC * kC * 2, kAhiB = 2 * kC * kC * 2, kAloB = 3 * kC * kC * 2, kKtB = 4 * kC * kC * 2;
 constexpr float kQs = 0.08838834764831845f;  // Dk^-1/2
 
 #define DAN_GLOBAL __attribute__((address_space(1)))
@@ -55,6 +72,7 @@ constexpr float kQs = 0.08838834764831845f;  // Dk^-1/2
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -135,8 +153,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
   const int L = min(kC, end - t0);
   const int hk = h / (p.Hv / p.Hk);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  constexpr bool kBf = std::is_same<T, __bf16>::value;
   float *rec = p.rec + ((int64_t)s * p.Hv + h) * kRec;
-  float *Tm = rec, *Am = rec + kC * kC, *vec = rec + 2 * kC * kC;
+  float *Tm = rec, *Am = rec + kC * kC, *vec = rec + (kBf ? kVecBf : kVecF32);
+  uint8_t *recb = reinterpret_cast<uint8_t *>(rec);
+  // x as the bf16 pair (hi, lo) at byte offsets hi_off / lo_off + 2 e
+  auto put_pair = [&](int hi_off, int lo_off, int e, float x) __attribute__((always_inline)) {
+    const __bf16 hi = (__bf16)x;
+    const __bf16 lo = (__bf16)(x - (float)hi);
+    *(DAN_GLOBAL __bf16 *)(recb + hi_off + 2 * e) = hi;
+    *(DAN_GLOBAL __bf16 *)(recb + lo_off + 2 * e) = lo;
+  };
 
   // wave 0: the gates of row `lane`, G by a prefix sum over the lanes, the row factors
   if (wave == 0) {
@@ -189,6 +216,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
     const u32x4 aq = *(const DAN_GLOBAL u32x4 *)(qi + 16 * kk);
     P = mfma_in<T>(a, b, P);
     QK = mfma_in<T>(aq, b, QK);
+    if constexpr (kBf) {
+      // K^T for the bf16 scan: row 32 bi + lane % 32 (clamped to the run; the
+      // scan multiplies padding columns by zero), d 16 kk + 8 (lane / 32) ..
+      if (bj == 0) {
+        const int row = 32 * bi + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *(DAN_GLOBAL uint16_t *)(recb + kKtB + 2 * ((16 * kk + 8 * (lane >> 5) + e) * kC + row)) =
+              (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
+      }
+    }
   }
   __syncthreads();  // sG and the row factors
 #pragma unroll
@@ -197,7 +235,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
     const float e = (i >= j && i < L) ? expf(sG[i] - sG[j]) : 0.f;
     const float rkj = sL[j][kC + 2];
     sL[i][j] = i > j ? sL[i][kC] * rkj * P[rr] * e : 0.f;
-    Am[i * kC + j] = sL[i][kC + 1] * rkj * QK[rr] * e;
+    const float av = sL[i][kC + 1] * rkj * QK[rr] * e;
+    if constexpr (kBf) put_pair(kAhiB, kAloB, i * kC + j, av);
+    else Am[i * kC + j] = av;
   }
   __syncthreads();
 
@@ -224,7 +264,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
       }
     }
 #pragma unroll
-    for (int k = 0; k < kC / 4; ++k) Tm[(4 * k + part) * kC + j] = xm[k];
+    for (int k = 0; k < kC / 4; ++k) {
+      if constexpr (kBf) put_pair(kThiB, kTloB, (4 * k + part) * kC + j, xm[k]);
+      else Tm[(4 * k + part) * kC + j] = xm[k];
+    }
   }
 }
 
@@ -327,7 +370,7 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
   auto load0 = [&](Ops<T, NC> &o, int t0, int s) __attribute__((always_inline)) {
     const int L = min(kC, end - t0);
     const int64_t tr = t0 + min(ri, L - 1);
-    const float *vec = rec_of(s) + 2 * kC * kC;
+    const float *vec = rec_of(s) + kVecF32;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.ka[j] = *(const DAN_GLOBAL u32x4 *)(kh + tr * p.k_st + 32 * j + 8 * q4);
 #pragma unroll
@@ -344,15 +387,15 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
     const float *rec = rec_of(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.ta[j] = *(const DAN_GLOBAL f32x4 *)(rec + ri * kC + 16 * j + 4 * q4);
-    o.vs = *(const DAN_GLOBAL f32x4 *)(rec + 2 * kC * kC + 3 * kC + ro);
+    o.vs = *(const DAN_GLOBAL f32x4 *)(rec + kVecF32 + 3 * kC + ro);
   };
   auto load2 = [&](Ops<T, NC> &o, int t0, int s) __attribute__((always_inline)) {
     const int L = min(kC, end - t0);
     const float *rec = rec_of(s);
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.aa[j] = *(const DAN_GLOBAL f32x4 *)(rec + kC * kC + ri * kC + 16 * j + 4 * q4);
-    o.vq = *(const DAN_GLOBAL f32x4 *)(rec + 2 * kC * kC + 2 * kC + ro);
-    o.glast = *(const DAN_GLOBAL float *)(rec + 2 * kC * kC + 4 * kC);
+    o.vq = *(const DAN_GLOBAL f32x4 *)(rec + kVecF32 + 2 * kC + ro);
+    o.glast = *(const DAN_GLOBAL float *)(rec + kVecF32 + 4 * kC);
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk)
       o.kt[kk] = *(const DAN_GLOBAL uint32_t *)(kh + (int64_t)(t0 + min(kidx64(kk, q4), L - 1)) * p.k_st + 32 * rb + 2 * l16);
@@ -485,6 +528,288 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
     *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols) = sS[(x / kCols) * kSS + x % kCols];
 }
 
+// ---------------------------------------------------------------- the bf16 scan
+// bf16 inputs: the same chunk step as chunk_scan_kernel, its products on
+// v_mfma_f32_16x16x32_bf16, eight times the fp32 product's rate. Every fp32
+// operand goes in as a bf16 pair (hi = bf16(x), lo = bf16(x - hi): ~16
+// significant bits); q, k and K^T are bf16 already. Per pair of operands:
+// K S, Q S, K^T Ds take two products (x hi, x lo), T Y and A D three (the lo
+// x lo term, ~2^-17 relative, is dropped). Sums stay fp32, and the state's
+// fp32 master copy carries the decay and the updates; the bf16 pairs of S are
+// rewritten from it every chunk.
+// LDS (bytes): the state's fp32 master [128][COLS + 2]; the state as bf16
+// planes (hi, lo) of [COLS][128 + 8] (one state column per row, so the B
+// operand's 8 consecutive state rows are 16 contiguous bytes); Y, D and
+// diag(exp(G_63 - G) r_k) D as planes of [COLS][64 + 8]. The 8-element pads
+// spread a B-operand read's 16 columns over the banks.
+template <int COLS>
+struct BfLds {
+  static constexpr int kSS = COLS + 2, kPS = kDk + 8, kPC = kC + 8;
+  static constexpr int sHi = kDk * kSS * 4, sLo = sHi + COLS * kPS * 2;
+  static constexpr int yHi = sLo + COLS * kPS * 2, yLo = yHi + COLS * kPC * 2;
+  static constexpr int dHi = yLo + COLS * kPC * 2, dLo = dHi + COLS * kPC * 2;
+  static constexpr int eHi = dLo + COLS * kPC * 2, eLo = eHi + COLS * kPC * 2;
+  static constexpr int bytes = eLo + COLS * kPC * 2;
+  static_assert(sHi % 16 == 0 && (kPS * 2) % 16 == 0 && (kPC * 2) % 16 == 0, "16-byte operand reads");
+};
+
+// State columns per work group of the bf16 scan, long and short runs alike:
+// its per-chunk operands (q, k, T, A, K^T) are loaded by every column group
+// of a (run, head), and with 16 columns the CUs' address units were the
+// limit (trunk phase of 5 runs of 286 to 1843 tokens: 0.209 ms on 16
+// columns, 0.164 on 32, 0.226 on 64 with one group per CU).
+constexpr int kBfCols = 32;
+
+__device__ inline f32x4 mma_bf(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+// x as a bf16 pair, the hi and lo halves' bits.
+__device__ inline void split_bf(float x, uint32_t &hi, uint32_t &lo) {
+  const __bf16 h = (__bf16)x;
+  const __bf16 l = (__bf16)(x - (float)h);
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, l);
+}
+// Four consecutive rows of one plane column (8 bytes, hi and lo planes).
+__device__ inline void put4_bf(uint8_t *hi_plane, uint8_t *lo_plane, int off, const f32x4 &x) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) split_bf(x[i], h[i], l[i]);
+  *reinterpret_cast<u32x2 *>(hi_plane + off) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  *reinterpret_cast<u32x2 *>(lo_plane + off) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+}
+
+// One wave's operands of one chunk, loaded a chunk ahead (each group right
+// after its last use in the chunk before).
+template <int NC>
+struct OpsBf {
+  u32x4 ka[4], qa[4];   // k, q row 16 rb + l16, d 32 j + 8 g4 .. + 7 (A operands of K S, Q S)
+  f32x4 va, vb, vq, vs; // the row factors of rows 16 rb + 4 g4 .. + 3
+  float vv[NC][4];      // v of those rows, the wave's columns
+  u32x4 th[2], tl[2];   // T row 16 rb + l16, chunk rows 32 j + 8 g4 .. + 7 (hi, lo)
+  u32x4 ah[2], al[2];   // A, the same
+  u32x4 kt[2][2];       // K^T row 32 rb + 16 mb + l16, chunk rows 32 j + 8 g4 .. + 7
+  float glast;
+};
+
+// Work group: one (run, value head, COLS state columns), 4 waves. Wave rb
+// computes rows 16 rb .. + 15 of Y, D and O and state rows 32 rb .. + 31,
+// all COLS columns (NC tiles of 16). Per chunk, with jmax = (L - 1) / 32:
+//   phase 0  K S and Q S (the S planes), Y to its planes                barrier
+//   phase 1  D = T Y (chunk-row blocks j <= rb / 2: T is lower triangular),
+//            D and Ds to their planes                                   barrier
+//   phase 2  O = (Q S) + A D; S <- gamma_63 S + K^T Ds (blocks j <= jmax)
+//            into the master and the S planes                           barrier
+// Padding rows (past the run) come out as zeros in Y, D and Ds (their row
+// factors are zero), so every wave runs every phase.
+template <int COLS>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+void chunk_scan_bf16_kernel(const Params p) {
+  constexpr int NC = COLS / 16;
+  using LB = BfLds<COLS>;
+  constexpr int kSS = LB::kSS, kPS = LB::kPS, kPC = LB::kPC;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LB::bytes];
+  float *sS = reinterpret_cast<float *>(lds);
+  const int b = blockIdx.x;
+  const int u = (b / (8 * p.ncb)) * 8 + (b & 7), cb = (b >> 3) % p.ncb;
+  if (u >= p.units) return;  // the whole group, before any barrier
+  const int r = u / p.Hv, h = u % p.Hv, hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, g4 = lane >> 4;
+  const int rb = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col0 = COLS * cb;
+  const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
+  for (int x = tid; x < kDk * COLS; x += 256) {
+    const int row = x / COLS, c = x % COLS;
+    const float v = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)row * p.Dv + c);
+    sS[row * kSS + c] = v;
+    uint32_t hi, lo;
+    split_bf(v, hi, lo);
+    *reinterpret_cast<uint16_t *>(lds + LB::sHi + 2 * (c * kPS + row)) = (uint16_t)hi;
+    *reinterpret_cast<uint16_t *>(lds + LB::sLo + 2 * (c * kPS + row)) = (uint16_t)lo;
+  }
+  const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
+  const __bf16 *qh = static_cast<const __bf16 *>(p.q) + (int64_t)hk * p.q_sh;
+  const __bf16 *kh = static_cast<const __bf16 *>(p.k) + (int64_t)hk * p.k_sh;
+  const __bf16 *vh = static_cast<const __bf16 *>(p.v) + (int64_t)h * p.v_sh + col0;
+  __bf16 *oh = static_cast<__bf16 *>(p.o) + (int64_t)h * p.o_sh + col0;
+  const int ri = 16 * rb + l16;     // the A-operand row of the 64-row products
+  const int ro = 16 * rb + 4 * g4;  // the first of the lane's accumulator rows
+
+  auto recb = [&](int s) __attribute__((always_inline)) {
+    return reinterpret_cast<const uint8_t *>(p.rec + ((int64_t)s * p.Hv + h) * kRec);
+  };
+  auto ld16 = [&](const uint8_t *q) __attribute__((always_inline)) { return *(const DAN_GLOBAL u32x4 *)q; };
+  auto load0 = [&](OpsBf<NC> &o, int t0, int s) __attribute__((always_inline)) {
+    const int L = min(kC, end - t0);
+    const int64_t tr = t0 + min(ri, L - 1);
+    const float *vec = reinterpret_cast<const float *>(recb(s)) + kVecBf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.ka[j] = *(const DAN_GLOBAL u32x4 *)(kh + tr * p.k_st + 32 * j + 8 * g4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.qa[j] = *(const DAN_GLOBAL u32x4 *)(qh + tr * p.q_st + 32 * j + 8 * g4);
+    o.va = *(const DAN_GLOBAL f32x4 *)(vec + 0 * kC + ro);
+    o.vb = *(const DAN_GLOBAL f32x4 *)(vec + 1 * kC + ro);
+#pragma unroll
+    for (int n = 0; n < NC; ++n)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        o.vv[n][rr] = (float)*(const DAN_GLOBAL __bf16 *)(vh + (int64_t)(t0 + min(ro + rr, L - 1)) * p.v_st + 16 * n + l16);
+  };
+  auto load1 = [&](OpsBf<NC> &o, int s) __attribute__((always_inline)) {
+    const uint8_t *rc = recb(s);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      o.th[j] = ld16(rc + kThiB + 2 * (ri * kC + 32 * j + 8 * g4));
+      o.tl[j] = ld16(rc + kTloB + 2 * (ri * kC + 32 * j + 8 * g4));
+    }
+    o.vs = *(const DAN_GLOBAL f32x4 *)(reinterpret_cast<const float *>(rc) + kVecBf + 3 * kC + ro);
+  };
+  auto load2 = [&](OpsBf<NC> &o, int s) __attribute__((always_inline)) {
+    const uint8_t *rc = recb(s);
+    const float *vec = reinterpret_cast<const float *>(rc) + kVecBf;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      o.ah[j] = ld16(rc + kAhiB + 2 * (ri * kC + 32 * j + 8 * g4));
+      o.al[j] = ld16(rc + kAloB + 2 * (ri * kC + 32 * j + 8 * g4));
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) o.kt[mb][j] = ld16(rc + kKtB + 2 * ((32 * rb + 16 * mb + l16) * kC + 32 * j + 8 * g4));
+    o.vq = *(const DAN_GLOBAL f32x4 *)(vec + 2 * kC + ro);
+    o.glast = *(const DAN_GLOBAL float *)(vec + 4 * kC);
+  };
+  // the 16 bytes of plane column c, rows k0 .. k0 + 7
+  auto rd = [&](int plane, int stride, int c, int k0) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4 *>(lds + plane + 2 * (c * stride + k0));
+  };
+
+  OpsBf<NC> op;
+  int s = r + row0 / kC;
+  if (row0 < end) {
+    load0(op, row0, s);
+    load1(op, s);
+    load2(op, s);
+  }
+  __syncthreads();
+  for (int t0 = row0; t0 < end; t0 += kC, ++s) {
+    const int L = min(kC, end - t0), jmax = (L - 1) >> 5;
+    const int jt = min(rb >> 1, jmax);  // the wave's last 32-row block of T Y and A D
+    const bool more = t0 + kC < end;    // the next chunk (this one again after the last: the loads stay in bounds)
+    const int tn = more ? t0 + kC : t0, sn = more ? s + 1 : s;
+
+    // phase 0: K S and Q S; Y = diag(beta) V - diag(beta gamma r_k) K S
+    f32x4 x[NC], o1[NC];
+#pragma unroll
+    for (int n = 0; n < NC; ++n) x[n] = o1[n] = f32x4{};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        const u32x4 bh = rd(LB::sHi, kPS, 16 * n + l16, 32 * j + 8 * g4);
+        const u32x4 bl = rd(LB::sLo, kPS, 16 * n + l16, 32 * j + 8 * g4);
+        x[n] = mma_bf(op.ka[j], bh, x[n]);
+        o1[n] = mma_bf(op.qa[j], bh, o1[n]);
+        x[n] = mma_bf(op.ka[j], bl, x[n]);
+        o1[n] = mma_bf(op.qa[j], bl, o1[n]);
+      }
+#pragma unroll
+    for (int n = 0; n < NC; ++n) {
+      f32x4 y;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) y[rr] = op.vb[rr] * op.vv[n][rr] - op.va[rr] * x[n][rr];
+      put4_bf(lds + LB::yHi, lds + LB::yLo, 2 * ((16 * n + l16) * kPC + ro), y);
+    }
+    load0(op, tn, sn);
+    barrier_lds();
+
+    // phase 1: D = T Y
+    {
+      f32x4 d[NC];
+#pragma unroll
+      for (int n = 0; n < NC; ++n) d[n] = f32x4{};
+#pragma unroll
+      for (int j = 0; j < 2; ++j)  // static indices keep op in registers; the guard is wave-uniform
+        if (j <= jt) {
+#pragma unroll
+          for (int n = 0; n < NC; ++n) {
+            const u32x4 bh = rd(LB::yHi, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            const u32x4 bl = rd(LB::yLo, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            d[n] = mma_bf(op.th[j], bh, d[n]);
+            d[n] = mma_bf(op.th[j], bl, d[n]);
+            d[n] = mma_bf(op.tl[j], bh, d[n]);
+          }
+        }
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        put4_bf(lds + LB::dHi, lds + LB::dLo, 2 * ((16 * n + l16) * kPC + ro), d[n]);
+        f32x4 e;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) e[rr] = op.vs[rr] * d[n][rr];
+        put4_bf(lds + LB::eHi, lds + LB::eLo, 2 * ((16 * n + l16) * kPC + ro), e);
+      }
+    }
+    load1(op, sn);
+    barrier_lds();
+
+    // phase 2: O = diag(r_q Dk^-1/2 gamma) Q S + A D; S <- gamma_63 S + K^T Ds
+    {
+      f32x4 o2[NC];
+#pragma unroll
+      for (int n = 0; n < NC; ++n) o2[n] = f32x4{};
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (j <= jt) {
+#pragma unroll
+          for (int n = 0; n < NC; ++n) {
+            const u32x4 bh = rd(LB::dHi, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            const u32x4 bl = rd(LB::dLo, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            o2[n] = mma_bf(op.ah[j], bh, o2[n]);
+            o2[n] = mma_bf(op.ah[j], bl, o2[n]);
+            o2[n] = mma_bf(op.al[j], bh, o2[n]);
+          }
+        }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (ro + rr < L) {
+#pragma unroll
+          for (int n = 0; n < NC; ++n)
+            *(DAN_GLOBAL __bf16 *)(oh + (int64_t)(t0 + ro + rr) * p.o_st + 16 * n + l16) = (__bf16)(op.vq[rr] * o1[n][rr] + o2[n][rr]);
+        }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int sr = 32 * rb + 16 * mb + 4 * g4;  // the lane's first state row of block mb
+      f32x4 acc[NC];
+#pragma unroll
+      for (int n = 0; n < NC; ++n)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) acc[n][rr] = op.glast * sS[(sr + rr) * kSS + 16 * n + l16];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (j <= jmax) {
+#pragma unroll
+          for (int n = 0; n < NC; ++n) {
+            const u32x4 bh = rd(LB::eHi, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            const u32x4 bl = rd(LB::eLo, kPC, 16 * n + l16, 32 * j + 8 * g4);
+            acc[n] = mma_bf(op.kt[mb][j], bh, acc[n]);
+            acc[n] = mma_bf(op.kt[mb][j], bl, acc[n]);
+          }
+        }
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sS[(sr + rr) * kSS + 16 * n + l16] = acc[n][rr];
+        put4_bf(lds + LB::sHi, lds + LB::sLo, 2 * ((16 * n + l16) * kPS + sr), acc[n]);
+      }
+    }
+    load2(op, sn);
+    barrier_lds();  // the new state is whole, and every read of this chunk's Y, D and S is done
+  }
+  for (int x = tid; x < kDk * COLS; x += 256)
+    *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / COLS) * p.Dv + x % COLS) = sS[(x / COLS) * kSS + x % COLS];
+}
+
 int64_t slots(int32_t num_tokens, int32_t num_runs) { return (int64_t)num_runs + num_tokens / kC; }
 
 }  // namespace dan_gdnc
@@ -519,8 +844,7 @@ hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t 
   constexpr int SW = dan_gdnc::kScanShortWaves, SC = dan_gdnc::kShortCols;
   if (a->dtype == DAN_DTYPE_BF16) {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<__bf16>, dim3((unsigned)prep), block, 0, s, p);
-    if (shortrun) scan(dan_gdnc::chunk_scan_kernel<__bf16, SW, SC>, SW, SC);
-    else scan(dan_gdnc::chunk_scan_kernel<__bf16, LW, LC>, LW, LC);
+    scan(dan_gdnc::chunk_scan_bf16_kernel<dan_gdnc::kBfCols>, 4, dan_gdnc::kBfCols);
   } else {
     if (prep) hipLaunchKernelGGL(dan_gdnc::chunk_prep_kernel<_Float16>, dim3((unsigned)prep), block, 0, s, p);
     if (shortrun) scan(dan_gdnc::chunk_scan_kernel<_Float16, SW, SC>, SW, SC);

@@ -80,7 +80,7 @@ int dan_gdn_fwd(const DanGdnArgs *args, void *stream);
 
 /* Workspace bytes for dan_gdn_fwd; 0 for arguments it would reject. The
  * token form's grows as 8 N Hk bytes, the chunked form's as
- * (R + N / 64) Hv 34 KiB. */
+ * (R + N / 64) Hv 49.25 KiB. */
 int64_t dan_gdn_workspace_size(int32_t form, int32_t num_tokens, int32_t num_runs, int32_t num_k_heads,
                                int32_t num_v_heads, int32_t v_dim);
 

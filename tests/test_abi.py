@@ -394,8 +394,9 @@ def test_gdn_form_and_workspace_errors(lib, kw, status, needle):
 def test_gdn_workspace_size(lib):
     norms = (1000 * 2 * 2 * 4 + 255) // 256 * 256
     assert lib.dan_gdn_workspace_size(_native.GDN_FORM_TOKEN, 1000, 3, 2, 4, 128) == norms
-    # chunk records: (runs + tokens // 64) slots x value heads x (T, A: 64 x 64 each, five rows of 64) floats
-    rec = (3 + 1000 // 64) * 4 * (2 * 64 * 64 + 5 * 64) * 4
+    # chunk records: (runs + tokens // 64) slots x value heads x (T and A as bf16 pairs, 64 x 64 each,
+    # K^T 128 x 64 bf16, five rows of 64 floats); the fp16 layout (T, A in fp32) fits in the same
+    rec = (3 + 1000 // 64) * 4 * ((4 * 64 * 64 * 2 + 128 * 64 * 2) // 4 + 5 * 64) * 4
     assert lib.dan_gdn_workspace_size(_native.GDN_FORM_CHUNK, 1000, 3, 2, 4, 128) == rec
     assert lib.dan_gdn_workspace_size(7, 1000, 3, 2, 4, 128) == 0
     assert lib.dan_gdn_workspace_size(_native.GDN_FORM_CHUNK, -1, 3, 2, 4, 128) == 0
