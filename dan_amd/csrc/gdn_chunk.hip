@@ -218,8 +218,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
     QK = mfma_in<T>(aq, b, QK);
     if constexpr (kBf) {
       // K^T for the bf16 scan: row 32 bi + lane % 32 (clamped to the run; the
-      // scan multiplies padding columns by zero), d 16 kk + 8 (lane / 32) ..
-      if (bj == 0) {
+      // scan multiplies padding columns by zero), d 16 kk + 8 (lane / 32) ..;
+      // the two waves of each row half split the k-steps
+      if ((kk >> 2) == bj) {
         const int row = 32 * bi + (lane & 31);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
