@@ -2,21 +2,21 @@
 // dan/models/qwen3_5.py:212-220 (DeltaNet._phase up to the delta rule) and
 // dan/fused.py:80-82 (delta_gates).
 //
-// Two launches, both HBM-bound streaming work:
-//   gdn_conv_kernel   one thread per (strip of kStrip output rows, 8 channels).
-//                     Consecutive threads take consecutive 16-byte channel
-//                     groups of the same rows, so every row load is coalesced.
-//                     A strip's window starts, ext entries and rows are each
-//                     loaded as one batch (all in flight), not one memory
-//                     round trip per row. Along a strip the K-row window
-//                     slides: output row i + 1 of a run starts one ext entry
-//                     after row i, so one new row is loaded per output row
-//                     and a full window only at a run boundary. Sum in fp32 (j = 0 .. K-1, fused
-//                     multiply-adds), rounded to the I/O type as the
-//                     reference's conv1d output is, then silu in fp32 (hardware
-//                     exp2 and reciprocal: the kernel is otherwise VALU-bound
-//                     on a full-precision exp and divide).
-//   gdn_gates_kernel  one thread per (output row, head): beta and g.
+// One launch of HBM-bound streaming work, gdn_conv_kernel:
+//   - its first work groups compute the gates, one thread per (output row,
+//     head): beta and g;
+//   - then one wave per (strip of kStrip output rows, 64 channel groups of 8
+//     channels). The lanes take consecutive 16-byte channel groups of the same
+//     rows, so every row load is coalesced, and the strip's window starts, ext
+//     entries and row bases are wave-uniform (scalar loads). A strip's window
+//     starts, ext entries and rows are each loaded as one batch (all in
+//     flight), not one memory round trip per row. Along a strip the K-row
+//     window slides: output row i + 1 of a run starts one ext entry after row
+//     i, so one new row is loaded per output row and a full window only at a
+//     run boundary. Sum in fp32 (j = 0 .. K-1, fused multiply-adds), rounded to
+//     the I/O type as the reference's conv1d output is, then silu in fp32
+//     (hardware exp2 and reciprocal: the kernel is otherwise VALU-bound on a
+//     full-precision exp and divide).
 // The packed projection rows are read in place through the virtual row index
 // (no concatenated copy of the source).
 #include <hip/hip_runtime.h>
@@ -32,7 +32,10 @@ extern thread_local char g_err[512];
 
 namespace dan_conv {
 
-constexpr int kStrip = 8;  // output rows per thread (16 held too many loads' registers: 2 waves per SIMD)
+// Output rows per wave. With the XCD-major order (shared window rows hit in
+// L2) and streaming stores, c3 trunk / branch phase: 4 rows 25.4 / 11.8 us,
+// 6 rows 25.4 / 12.5, 8 rows 25.6 / 12.9; 16 rows held too many registers.
+constexpr int kStrip = 4;
 constexpr int kBlock = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -70,53 +73,88 @@ struct Params {
   float *beta, *g;
   int64_t src_stride, out_stride, b_stride, a_stride;
   int32_t C, N, hist_rows, num_ext, T, Hv, groups;  // groups = C / 8
+  int32_t cblocks, gate_blocks;  // ceil(groups / 64) waves per strip; work groups of gates
 };
 
-// 8 channels of virtual source row e (zeros outside the packed and history rows).
-template <typename T>
-__device__ inline f32x8 load_row(const Params &p, int e, int cg) {
-  const T *row = nullptr;
-  if (e >= 0 && e < p.N)
-    row = static_cast<const T *>(p.src) + (int64_t)e * p.src_stride;
-  else if (e > p.N && e - p.N - 1 < p.hist_rows)
-    row = static_cast<const T *>(p.hist) + (int64_t)(e - p.N - 1) * p.C;
-  if (!row) return f32x8{0, 0, 0, 0, 0, 0, 0, 0};
-  return cvt8<T>(*(const DAN_GLOBAL u32x4 *)(row + 8 * cg));
+// A wave-uniform int32 table entry through the scalar unit (the tables are
+// read-only during the launch).
+__device__ inline int sload(const int32_t *p) {
+  return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t *)p);
 }
 
+// beta and g of output row i and value head h (one work item of the gates).
+template <typename T>
+__device__ inline void gates(const Params &p, int64_t gid) {
+  if (gid >= (int64_t)p.T * p.Hv) return;
+  const int i = (int)(gid / p.Hv), h = (int)(gid % p.Hv);
+  const int r = p.rows[i];
+  float beta = 0.0f, g = 0.0f;
+  if (r >= 0 && r < p.N) {
+    const float bb = (float)static_cast<const T *>(p.b)[(int64_t)r * p.b_stride + h];
+    const float aa = (float)static_cast<const T *>(p.a)[(int64_t)r * p.a_stride + h];
+    beta = (float)(T)(1.0f / (1.0f + expf(-bb)));
+    const float z = aa + p.dt_bias[h];
+    const float sp = z > 20.0f ? z : log1pf(expf(z));  // softplus, threshold 20
+    g = -expf(p.a_log[h]) * sp;
+  }
+  p.beta[gid] = beta;
+  p.g[gid] = g;
+}
+
+// The first gate_blocks work groups compute the gates (they are dispatched
+// first and overlap the conv's streaming); every other wave takes one strip of
+// kStrip output rows and 64 consecutive channel groups, so its window starts,
+// ext entries and row bases are wave-uniform: scalar loads, and row loads on a
+// scalar base plus the lane's channel offset.
 template <typename T, int K>
 __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
-  const int64_t gid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const int cg = (int)(gid % p.groups);
-  const int64_t i0 = gid / p.groups * kStrip;
-  if (i0 >= p.T) return;
-  const int nr = (int)min((int64_t)p.T - i0, (int64_t)kStrip);  // output rows of this strip
-  f32x8 w[K];
+  if ((int)blockIdx.x < p.gate_blocks) {
+    gates<T>(p, (int64_t)blockIdx.x * kBlock + threadIdx.x);
+    return;
+  }
+  // Work groups go to the 8 XCDs (each with its own L2) in turn: XCD-major
+  // order gives each XCD a contiguous range of strips, so the K - 1 window
+  // rows that a strip shares with the one before it are L2 hits.
+  const int i = (int)blockIdx.x - p.gate_blocks, nb = (int)gridDim.x - p.gate_blocks;
+  const int blk = i % 8 * (nb / 8) + min(i % 8, nb % 8) + i / 8;
+  const int wave = __builtin_amdgcn_readfirstlane(blk * (kBlock / 64) + (int)(threadIdx.x >> 6));
+  const int i0 = wave / p.cblocks * kStrip;
+  const int cg = wave % p.cblocks * 64 + (int)(threadIdx.x & 63);
+  if (i0 >= p.T || cg >= p.groups) return;
+  const int nr = min(p.T - i0, kStrip);  // output rows of this strip
+  // The 8 channels' taps, [channel][tap] as stored, kept packed (converted
+  // where used: registers are what limits the waves per SIMD here).
+  T wr[8 * K] __attribute__((aligned(16)));
   const T *wp = static_cast<const T *>(p.weight) + (int64_t)cg * 8 * K;
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
+  for (int i = 0; i < K; ++i)  // 16 bytes = 8 values per load
+    *reinterpret_cast<u32x4 *>(wr + 8 * i) = *(const DAN_GLOBAL u32x4 *)(wp + 8 * i);
+  T *out = static_cast<T *>(p.out) + (int64_t)i0 * p.out_stride + 8 * cg;
+  // x: the window's K rows as raw packed values, converted here.
+  auto emit = [&](int r, const u32x4(&x)[K]) __attribute__((always_inline)) {
+    f32x8 xs[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) w[j][c] = (float)wp[c * K + j];
-  T *out = static_cast<T *>(p.out) + i0 * p.out_stride + 8 * cg;
-  auto emit = [&](int r, const f32x8(&x)[K]) __attribute__((always_inline)) {
+    for (int j = 0; j < K; ++j) xs[j] = cvt8<T>(x[j]);
     f32x8 y;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      float acc = w[0][c] * x[0][c];
+      float acc = (float)wr[c * K] * xs[0][c];
 #pragma unroll
-      for (int j = 1; j < K; ++j) acc = fmaf(w[j][c], x[j][c], acc);
+      for (int j = 1; j < K; ++j) acc = fmaf((float)wr[c * K + j], xs[j][c], acc);
       const float r = (float)(T)acc;  // the conv output in the I/O type
       // silu(r) = r / (1 + e^-r) with the hardware exp2 and reciprocal (about
       // one fp32 ulp each, far below the output type's spacing)
       y[c] = r * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(r * -1.4426950408889634f));
     }
-    *(DAN_GLOBAL u32x4 *)(out + (int64_t)r * p.out_stride) = pack8<T>(y);
+    // streaming store: nothing in this launch reads the output
+    __builtin_nontemporal_store(pack8<T>(y), (DAN_GLOBAL u32x4 *)(out + (int64_t)r * p.out_stride));
   };
+  const u32x4 zero = {0, 0, 0, 0};
   // With no source row or too few ext entries every window reads as zeros.
   if (!((p.N > 0 || p.hist_rows > 0) && p.num_ext >= K)) {
-    f32x8 x[K];
+    u32x4 x[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) x[j] = f32x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < K; ++j) x[j] = zero;
     for (int r = 0; r < nr; ++r) emit(r, x);
     return;
   }
@@ -137,7 +175,7 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
   int t[kStrip];
   bool tv[kStrip];
 #pragma unroll
-  for (int r = 0; r < kStrip; ++r) t[r] = p.take[i0 + min(r, nr - 1)];
+  for (int r = 0; r < kStrip; ++r) t[r] = sload(p.take + i0 + min(r, nr - 1));
 #pragma unroll
   for (int r = 0; r < kStrip; ++r) {
     tv[r] = t[r] >= 0 && t[r] <= p.num_ext - K;
@@ -146,9 +184,9 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
   // 2. Each row's newest window entry, and the first row's older ones.
   int en[kStrip], ep[K - 1];
 #pragma unroll
-  for (int r = 0; r < kStrip; ++r) en[r] = p.ext[t[r] + K - 1];
+  for (int r = 0; r < kStrip; ++r) en[r] = sload(p.ext + t[r] + K - 1);
 #pragma unroll
-  for (int j = 0; j < K - 1; ++j) ep[j] = p.ext[t[0] + j];
+  for (int j = 0; j < K - 1; ++j) ep[j] = sload(p.ext + t[0] + j);
   // 3. Their rows.
   u32x4 rn[kStrip], rp[K - 1];
   bool okn[kStrip], okp[K - 1];
@@ -156,13 +194,12 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
   for (int r = 0; r < kStrip; ++r) rn[r] = row_at(en[r], okn[r]);
 #pragma unroll
   for (int j = 0; j < K - 1; ++j) rp[j] = row_at(ep[j], okp[j]);
-  const f32x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   // 4. The outputs. Along a run the window slides one entry per output row;
   //    at a run boundary (rare) the row's older entries are loaded then.
-  f32x8 x[K];
+  u32x4 x[K];
 #pragma unroll
-  for (int j = 0; j < K - 1; ++j) x[j] = tv[0] && okp[j] ? cvt8<T>(rp[j]) : zero;
-  x[K - 1] = tv[0] && okn[0] ? cvt8<T>(rn[0]) : zero;
+  for (int j = 0; j < K - 1; ++j) x[j] = tv[0] && okp[j] ? rp[j] : zero;
+  x[K - 1] = tv[0] && okn[0] ? rn[0] : zero;
   emit(0, x);
 #pragma unroll
   for (int r = 1; r < kStrip; ++r) {
@@ -174,47 +211,20 @@ __global__ __launch_bounds__(kBlock) void gdn_conv_kernel(const Params p) {
 #pragma unroll
       for (int j = 0; j < K - 1; ++j) {
         bool ok = false;
-        const u32x4 raw = tv[r] ? row_at(p.ext[t[r] + j], ok) : u32x4{0, 0, 0, 0};
-        x[j] = ok ? cvt8<T>(raw) : zero;
+        const u32x4 raw = tv[r] ? row_at(sload(p.ext + t[r] + j), ok) : zero;
+        x[j] = ok ? raw : zero;
       }
     }
-    x[K - 1] = tv[r] && okn[r] ? cvt8<T>(rn[r]) : zero;
+    x[K - 1] = tv[r] && okn[r] ? rn[r] : zero;
     if (r < nr) emit(r, x);
   }
 }
 
 template <typename T>
-__global__ __launch_bounds__(kBlock) void gdn_gates_kernel(const Params p) {
-  const int64_t gid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (gid >= (int64_t)p.T * p.Hv) return;
-  const int i = (int)(gid / p.Hv), h = (int)(gid % p.Hv);
-  const int r = p.rows[i];
-  float beta = 0.0f, g = 0.0f;
-  if (r >= 0 && r < p.N) {
-    const float bb = (float)static_cast<const T *>(p.b)[(int64_t)r * p.b_stride + h];
-    const float aa = (float)static_cast<const T *>(p.a)[(int64_t)r * p.a_stride + h];
-    beta = (float)(T)(1.0f / (1.0f + expf(-bb)));
-    const float z = aa + p.dt_bias[h];
-    const float sp = z > 20.0f ? z : log1pf(expf(z));  // softplus, threshold 20
-    g = -expf(p.a_log[h]) * sp;
-  }
-  p.beta[gid] = beta;
-  p.g[gid] = g;
-}
-
-template <typename T, int K>
-void launch_conv(const Params &p, int64_t grid, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_conv_kernel<T, K>), dim3((unsigned)grid), dim3(kBlock), 0, s, p);
-}
-
-template <typename T>
-void launch(const Params &p, int K, int64_t grid, int64_t ggrid, hipStream_t s) {
-  if (grid) {
-    if (K == 2) launch_conv<T, 2>(p, grid, s);
-    else if (K == 3) launch_conv<T, 3>(p, grid, s);
-    else launch_conv<T, 4>(p, grid, s);
-  }
-  if (ggrid) hipLaunchKernelGGL(gdn_gates_kernel<T>, dim3((unsigned)ggrid), dim3(kBlock), 0, s, p);
+void launch(const Params &p, int K, int64_t grid, hipStream_t s) {
+  if (K == 2) hipLaunchKernelGGL((gdn_conv_kernel<T, 2>), dim3((unsigned)grid), dim3(kBlock), 0, s, p);
+  else if (K == 3) hipLaunchKernelGGL((gdn_conv_kernel<T, 3>), dim3((unsigned)grid), dim3(kBlock), 0, s, p);
+  else hipLaunchKernelGGL((gdn_conv_kernel<T, 4>), dim3((unsigned)grid), dim3(kBlock), 0, s, p);
 }
 
 }  // namespace dan_conv
@@ -236,6 +246,7 @@ extern "C" int dan_gdn_conv(const DanGdnConvArgs *a, void *stream) {
   if (((uintptr_t)a->src & 15) || ((uintptr_t)a->hist & 15) || ((uintptr_t)a->out & 15) || a->src_stride % 8 ||
       a->out_stride % 8 || a->src_stride < a->channels || a->out_stride < a->channels)
     return fail(DAN_ERR_INVALID_ARGUMENT, "src, hist and out rows must be 16-byte aligned and hold the channels");
+  if ((uintptr_t)a->weight & 15) return fail(DAN_ERR_INVALID_ARGUMENT, "weight must be 16-byte aligned");
   if (a->num_heads && (!a->rows || !a->b || !a->a || !a->a_log || !a->dt_bias || !a->beta || !a->g))
     return fail(DAN_ERR_INVALID_ARGUMENT, "NULL gate pointer");
   dan_conv::Params p;
@@ -245,13 +256,16 @@ extern "C" int dan_gdn_conv(const DanGdnConvArgs *a, void *stream) {
   p.src_stride = a->src_stride; p.out_stride = a->out_stride; p.b_stride = a->b_stride; p.a_stride = a->a_stride;
   p.C = a->channels; p.N = a->num_rows; p.hist_rows = a->num_hist_rows; p.num_ext = a->num_ext; p.T = a->num_out;
   p.Hv = a->num_heads; p.groups = a->channels / 8;
-  const int64_t threads = (int64_t)(a->num_out + dan_conv::kStrip - 1) / dan_conv::kStrip * p.groups;
-  const int64_t grid = (threads + dan_conv::kBlock - 1) / dan_conv::kBlock;
-  const int64_t ggrid = ((int64_t)a->num_out * a->num_heads + dan_conv::kBlock - 1) / dan_conv::kBlock;
-  if (grid > 0x7fffffff || ggrid > 0x7fffffff) return fail(DAN_ERR_INVALID_ARGUMENT, "too many rows x channels");
+  p.cblocks = (p.groups + 63) / 64;
+  const int64_t waves = (int64_t)(a->num_out + dan_conv::kStrip - 1) / dan_conv::kStrip * p.cblocks;
+  const int64_t gate_blocks = ((int64_t)a->num_out * a->num_heads + dan_conv::kBlock - 1) / dan_conv::kBlock;
+  const int64_t grid = gate_blocks + (waves + dan_conv::kBlock / 64 - 1) / (dan_conv::kBlock / 64);
+  if (grid > 0x7fffffff / (dan_conv::kBlock / 64) || a->num_out > 0x7fffffff - dan_conv::kStrip)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "too many rows x channels");
+  p.gate_blocks = (int32_t)gate_blocks;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a->dtype == DAN_DTYPE_BF16) dan_conv::launch<__bf16>(p, a->kernel, grid, ggrid, s);
-  else dan_conv::launch<_Float16>(p, a->kernel, grid, ggrid, s);
+  if (a->dtype == DAN_DTYPE_BF16) dan_conv::launch<__bf16>(p, a->kernel, grid, s);
+  else dan_conv::launch<_Float16>(p, a->kernel, grid, s);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(DAN_ERR_LAUNCH, "conv launch failed: %s", hipGetErrorString(err));
   return DAN_OK;

@@ -235,6 +235,8 @@ def conv_phase_args(qkv, hist, ph, weight, b, a, a_log, dt_bias):
     if qkv.stride(1) != 1 or qkv.stride(0) % 8 or qkv.data_ptr() % 16:
         qkv = qkv.contiguous()
     w = weight.reshape(c, kk).to(qkv.dtype).contiguous()
+    if w.data_ptr() % 16:
+        w = w.clone()
     hist = None if hist is None else hist.to(qkv.dtype).contiguous()
     b = b if b.stride(1) == 1 else b.contiguous()
     a = a if a.stride(1) == 1 else a.contiguous()

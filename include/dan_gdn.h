@@ -111,7 +111,7 @@ typedef struct {
   const void *hist;                     /* [num_hist_rows, C] contiguous */
   const int32_t *ext;                   /* [num_ext] virtual source rows */
   const int32_t *take;                  /* [T] first ext entry of output row i's window */
-  const void *weight;                   /* [C, K] (nn.Conv1d's [C, 1, K]) */
+  const void *weight;                   /* [C, K] (nn.Conv1d's [C, 1, K]), 16-byte aligned */
   void *out; int64_t out_stride;        /* [T, C] */
   int32_t num_heads;                    /* Hv; 0 skips the gates */
   int32_t reserved;

@@ -424,6 +424,7 @@ def _conv_args(**kw):
     (dict(channels=36), _native.ERR_UNSUPPORTED, "channels"),
     (dict(num_ext=-1), _native.ERR_INVALID_ARGUMENT, "negative"),
     (dict(), _native.ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(src=4096, ext=4096, take=4096, weight=4098, out=8192), _native.ERR_INVALID_ARGUMENT, "weight must be"),
 ])
 def test_gdn_conv_argument_errors(lib, kw, status, needle):
     rc = lib.dan_gdn_conv(ctypes.byref(_conv_args(**kw)), None)

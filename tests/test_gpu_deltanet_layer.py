@@ -90,19 +90,22 @@ def test_conv_phase_matches_oracle(gpu, dtype):
 
 
 
+@pytest.mark.parametrize("c", [64, 576])
 @pytest.mark.parametrize("kernel", [2, 3, 4])
 @pytest.mark.parametrize("n_rows, n_hist, n_ext, n_out, mode",
                          [(300, 3, 320, 251, "runs"), (120, 0, 130, 37, "wild"), (0, 5, 12, 21, "runs"),
                           (64, 2, 80, 1, "runs"), (17, 1, 3, 20, "wild")])
-def test_conv_table_edges(gpu, kernel, n_rows, n_hist, n_ext, n_out, mode):
+def test_conv_table_edges(gpu, kernel, n_rows, n_hist, n_ext, n_out, mode, c):
     """dan_gdn_conv on hand-made tables: runs whose boundaries fall inside a
-    thread's strip of output rows, a ragged last strip, window starts and ext
+    wave's strip of output rows, a ragged last strip, window starts and ext
     entries outside their ranges (zero windows and zero rows), no packed rows,
-    and fewer ext entries than a window. Against silu_conv over the virtual
-    source the ABI defines (packed row e, zeros at e == N, history row
-    e - N - 1, zeros elsewhere)."""
-    dtype, c, hv = torch.bfloat16, 64, 2
-    say(f"conv table K {kernel} N {n_rows} hist {n_hist} ext {n_ext} T {n_out} {mode}")
+    and fewer ext entries than a window. Channel widths of 64 (8 of a wave's
+    64 channel groups) and 576 (a strip over two waves, the second one
+    partly filled). Against silu_conv over the virtual source the ABI defines
+    (packed row e, zeros at e == N, history row e - N - 1, zeros
+    elsewhere)."""
+    dtype, hv = torch.bfloat16, 2
+    say(f"conv table C {c} K {kernel} N {n_rows} hist {n_hist} ext {n_ext} T {n_out} {mode}")
     g = torch.Generator().manual_seed(11 + kernel + n_out)
     proj = torch.randn(max(n_rows, 1), c + 16, generator=g).to(dtype)
     hist = torch.randn(max(n_hist, 1), c, generator=g).to(dtype)
