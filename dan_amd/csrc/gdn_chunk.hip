@@ -14,14 +14,15 @@
 //   O = diag(r_q Dk^-1/2 gamma) Q S + A D
 //   S <- gamma_63 S + K^T diag(exp(G_63 - G) r_k) D
 // Two launches:
-//   chunk_prep_kernel  every (chunk, value head) at once: the l2-norm factors
-//                      of the chunk's q and k rows, K K^T and Q K^T on
-//                      v_mfma_f32_32x32x16 (exact bf16/fp16 products, fp32
-//                      sums; the norm factors and decays are applied after,
-//                      in fp32), then T by forward substitution, one column
-//                      per four lanes; T, A and the per-row factors (and for
-//                      bf16 inputs K^T) go to the chunk records of the
-//                      workspace.
+//   chunk_prep_kernel  every (chunk, value head) at once: the chunk's q and k
+//                      rows into LDS in coalesced loads, the l2-norm factors
+//                      of the rows, K K^T and Q K^T on v_mfma_f32_32x32x16
+//                      (exact bf16/fp16 products, fp32 sums; the norm factors
+//                      and decays are applied after, in fp32), then T by
+//                      forward substitution, one column per four lanes; T, A
+//                      and the per-row factors (and for bf16 inputs K^T) go
+//                      to the chunk records of the workspace, T and A staged
+//                      in LDS for 16-byte stores.
 //   chunk_scan_bf16_kernel  (bf16 inputs) one work group per (run, value
 //                      head, 32 state columns), the state slice in LDS; the
 //                      run's chunks in order, each the five products above on
@@ -125,61 +126,119 @@ __device__ inline float sumsq8(u32x4 x) {
 __device__ inline int slot_of(const int32_t *cu, int r) { return r + *(const DAN_GLOBAL int32_t *)(cu + r) / kC; }
 
 // ---------------------------------------------------------------- chunk preparation
+// A work-group barrier that waits for this wave's LDS operations only:
+// __syncthreads() also waits for every global access in flight (the scan's
+// next-chunk operand loads, the prep's record stores).
+__device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The prep's LDS: the chunk's k and q rows, 16 threads per row loading 16
+// bytes each (coalesced; the products then read their operands here). Rows
+// are kTileRow bytes apart: 16 rows reading 16 bytes of one column hit all 64
+// banks. After the products the q tile holds L [64][kC + 4] (the same bytes)
+// and the k tile stages A, then T: 16 KB each, written to the record in
+// coalesced 16-byte stores.
+constexpr int kTileRow = kDk * 2 + 16;
+constexpr int kTileBytes = kC * kTileRow;
+static_assert(kTileBytes == kC * (kC + 4) * 4, "L fits the q tile");
+static_assert(kC * kC * 4 <= kTileBytes, "A or T staging fits the k tile");
+
+// Rows 16 W .. kC - 1 of the forward substitution (rows above 16 W are 0 in
+// wave W's columns), as one straight-line block.
+template <int W>
+__device__ inline void tsolve_rows(const float (*sL)[kC + 4], float (&xm)[kC / 4], int j, int part) {
+#pragma unroll
+  for (int i = 16 * W; i < kC; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < (i + 3) / 4; ++k) acc = fmaf(sL[i][4 * k + part], xm[k], acc);
+    acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0xB1, 0xf, 0xf, false));
+    acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x4E, 0xf, 0xf, false));
+    const float xi = (i == j ? 1.f : 0.f) - acc;
+    if (part == (i & 3)) xm[i >> 2] = xi;
+  }
+}
+
 // Grid: slots x Hv; a slot past its run's last chunk exits at once.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
-  __shared__ float sL[kC][kC + 4];
-  __shared__ float sG[kC];
+  __shared__ __attribute__((aligned(16))) uint8_t sKt[kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t sQt[kTileBytes];
+  __shared__ float sG[kC], sF[3][kC];  // G; per row beta r_k, r_q Dk^-1/2 and r_k
+  float(*sL)[kC + 4] = reinterpret_cast<float(*)[kC + 4]>(sQt);
   const int s = blockIdx.x / p.Hv, h = blockIdx.x % p.Hv;
   // The run of slot s: the largest r with slot_of(r) <= s. slot_of increases
   // strictly with r (slot_of(0) = 0), so r + 1 is the number of runs whose
   // slot is at most s: each wave counts them 64 runs at a time with one load
   // per lane, all in flight, instead of a binary search's chain of loads.
-  int r = 0;
+  // The same pass loads cu[r] and cu[r + 1] (the lane of run r holds them).
+  int r = 0, cu_r = 0, cu_r1 = 0;
   {
     const int ln = threadIdx.x & 63;
+    int last0 = 0, last1 = 0;  // cu[base - 1], cu[base]: lane 63 of the pass before
     for (int base = 0; base < p.R; base += 64) {
-      const int rr = base + ln;
-      const bool le = rr < p.R && slot_of(p.cu, min(rr, p.R - 1)) <= s;
+      const int rr = min(base + ln, p.R - 1);
+      const int c0 = *(const DAN_GLOBAL int32_t *)(p.cu + rr), c1 = *(const DAN_GLOBAL int32_t *)(p.cu + rr + 1);
+      const bool le = base + ln < p.R && rr + c0 / kC <= s;
       const uint64_t m = __ballot(le);
-      r = base + __popcll(m) - 1;
+      const int n = __popcll(m);
+      r = base + n - 1;
+      cu_r = n > 0 ? __shfl(c0, n - 1) : last0;
+      cu_r1 = n > 0 ? __shfl(c1, n - 1) : last1;
+      last0 = __shfl(c0, 63);
+      last1 = __shfl(c1, 63);
       if (m != ~0ull) break;  // a run of this block starts past s (or the runs end here)
     }
-    r = max(r, 0);
   }
-  const int t0 = *(const DAN_GLOBAL int32_t *)(p.cu + r) + kC * (s - slot_of(p.cu, r));
-  const int end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
+  const int t0 = cu_r + kC * (s - (r + cu_r / kC));
+  const int end = cu_r1;
   if (t0 >= end) return;  // the whole group, before any barrier
   const int L = min(kC, end - t0);
   const int hk = h / (p.Hv / p.Hk);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   constexpr bool kBf = std::is_same<T, __bf16>::value;
   float *rec = p.rec + ((int64_t)s * p.Hv + h) * kRec;
-  float *Tm = rec, *Am = rec + kC * kC, *vec = rec + (kBf ? kVecBf : kVecF32);
+  float *vec = rec + (kBf ? kVecBf : kVecF32);
   uint8_t *recb = reinterpret_cast<uint8_t *>(rec);
-  // x as the bf16 pair (hi, lo) at byte offsets hi_off / lo_off + 2 e
-  auto put_pair = [&](int hi_off, int lo_off, int e, float x) __attribute__((always_inline)) {
-    const __bf16 hi = (__bf16)x;
-    const __bf16 lo = (__bf16)(x - (float)hi);
-    *(DAN_GLOBAL __bf16 *)(recb + hi_off + 2 * e) = hi;
-    *(DAN_GLOBAL __bf16 *)(recb + lo_off + 2 * e) = lo;
-  };
 
-  // wave 0: the gates of row `lane`, G by a prefix sum over the lanes, the row factors
+  // 1. The k and q rows (rows past the run repeat its last row; the scan
+  //    multiplies padding by zero), and wave 0's gates of row `lane`.
+  {
+    const T *kb = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh + 8 * (tid & 15);
+    const T *qb = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh + 8 * (tid & 15);
+    u32x4 kx[4], qx[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int64_t t = t0 + min(16 * m + (tid >> 4), L - 1);
+      kx[m] = *(const DAN_GLOBAL u32x4 *)(kb + t * p.k_st);
+      qx[m] = *(const DAN_GLOBAL u32x4 *)(qb + t * p.q_st);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int at = (16 * m + (tid >> 4)) * kTileRow + 16 * (tid & 15);
+      *reinterpret_cast<u32x4 *>(sKt + at) = kx[m];
+      *reinterpret_cast<u32x4 *>(sQt + at) = qx[m];
+    }
+  }
+  float G = 0.f, b = 0.f;
+  if (wave == 0) {
+    const bool ok = lane < L;
+    const int64_t t = t0 + min(lane, L - 1);
+    G = ok ? *(const DAN_GLOBAL float *)(p.g + t * p.Hv + h) : 0.f;
+    b = ok ? *(const DAN_GLOBAL float *)(p.beta + t * p.Hv + h) : 0.f;
+  }
+  barrier_lds();
+
+  // 2. Wave 0: the row factors of row `lane`: 1 / sqrt(sum x^2 + 1e-6) of its
+  //    q and k rows (dan/models/qwen3_5.py:99-100), G by a prefix sum over the
+  //    lanes, the record's five rows.
   if (wave == 0) {
     const int i = lane;
     const bool ok = i < L;
-    const int64_t t = t0 + min(i, L - 1);
-    float G = ok ? *(const DAN_GLOBAL float *)(p.g + t * p.Hv + h) : 0.f;
-    const float b = ok ? *(const DAN_GLOBAL float *)(p.beta + t * p.Hv + h) : 0.f;
-    // 1 / sqrt(sum x^2 + 1e-6) of row t of q and of k (dan/models/qwen3_5.py:99-100)
-    const T *qr = static_cast<const T *>(p.q) + t * p.q_st + (int64_t)hk * p.q_sh;
-    const T *kr = static_cast<const T *>(p.k) + t * p.k_st + (int64_t)hk * p.k_sh;
     float sq = 0.f, sk = 0.f;
 #pragma unroll
     for (int j = 0; j < kDk / 8; ++j) {
-      sq += sumsq8<T>(*(const DAN_GLOBAL u32x4 *)(qr + 8 * j));
-      sk += sumsq8<T>(*(const DAN_GLOBAL u32x4 *)(kr + 8 * j));
+      sq += sumsq8<T>(*reinterpret_cast<const u32x4 *>(sQt + i * kTileRow + 16 * j));
+      sk += sumsq8<T>(*reinterpret_cast<const u32x4 *>(sKt + i * kTileRow + 16 * j));
     }
     const float rq = ok ? 1.0f / sqrtf(sq + 1e-6f) : 0.f;
     const float rk = ok ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
@@ -196,79 +255,106 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(const Params p) {
     vec[2 * kC + i] = rq * kQs * gam;
     vec[3 * kC + i] = expf(Glast - G) * rk;
     vec[4 * kC + i] = i == 0 ? expf(Glast) : 0.f;
-    sL[i][kC] = b * rk;  // spare columns: beta r_k, r_q Dk^-1/2 and r_k of row i
-    sL[i][kC + 1] = rq * kQs;
-    sL[i][kC + 2] = rk;
+    sF[0][i] = b * rk;
+    sF[1][i] = rq * kQs;
+    sF[2][i] = rk;
   }
 
   // K K^T and Q K^T, 32 x 32 block (bi, bj) per wave: lane l reads 16 bytes
   // of row 32 b + l % 32 at element 16 kk + 8 (l / 32).
   const int bi = wave >> 1, bj = wave & 1;
-  const int64_t ri = t0 + min(32 * bi + (lane & 31), L - 1), rj = t0 + min(32 * bj + (lane & 31), L - 1);
-  const T *ki = static_cast<const T *>(p.k) + ri * p.k_st + (int64_t)hk * p.k_sh + 8 * (lane >> 5);
-  const T *kj = static_cast<const T *>(p.k) + rj * p.k_st + (int64_t)hk * p.k_sh + 8 * (lane >> 5);
-  const T *qi = static_cast<const T *>(p.q) + ri * p.q_st + (int64_t)hk * p.q_sh + 8 * (lane >> 5);
+  const uint8_t *ki = sKt + (32 * bi + (lane & 31)) * kTileRow + 16 * (lane >> 5);
+  const uint8_t *kj = sKt + (32 * bj + (lane & 31)) * kTileRow + 16 * (lane >> 5);
+  const uint8_t *qi = sQt + (32 * bi + (lane & 31)) * kTileRow + 16 * (lane >> 5);
   f32x16 P = {}, QK = {};
 #pragma unroll
   for (int kk = 0; kk < kDk / 16; ++kk) {
-    const u32x4 a = *(const DAN_GLOBAL u32x4 *)(ki + 16 * kk);
-    const u32x4 b = *(const DAN_GLOBAL u32x4 *)(kj + 16 * kk);
-    const u32x4 aq = *(const DAN_GLOBAL u32x4 *)(qi + 16 * kk);
-    P = mfma_in<T>(a, b, P);
-    QK = mfma_in<T>(aq, b, QK);
-    if constexpr (kBf) {
-      // K^T for the bf16 scan: row 32 bi + lane % 32 (clamped to the run; the
-      // scan multiplies padding columns by zero), d 16 kk + 8 (lane / 32) ..;
-      // the two waves of each row half split the k-steps
-      if ((kk >> 2) == bj) {
-        const int row = 32 * bi + (lane & 31);
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(ki + 32 * kk);
+    const u32x4 bb = *reinterpret_cast<const u32x4 *>(kj + 32 * kk);
+    const u32x4 aq = *reinterpret_cast<const u32x4 *>(qi + 32 * kk);
+    P = mfma_in<T>(a, bb, P);
+    QK = mfma_in<T>(aq, bb, QK);
+  }
+  if constexpr (kBf) {
+    // K^T [Dk][kC] for the bf16 scan: thread t writes d rows 2 dp and 2 dp + 1,
+    // tokens 8 oc .. 8 oc + 7, from 8 dwords (d 2 dp, 2 dp + 1) of 8 tile rows.
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *(DAN_GLOBAL uint16_t *)(recb + kKtB + 2 * ((16 * kk + 8 * (lane >> 5) + e) * kC + row)) =
-              (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
+    for (int n = 0; n < 2; ++n) {
+      const int dp = (tid >> 3) + 32 * n, oc = tid & 7;
+      uint32_t w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = *reinterpret_cast<const uint32_t *>(sKt + (8 * oc + e) * kTileRow + 4 * dp);
+      u32x4 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = (w[2 * e] & 0xffffu) | (w[2 * e + 1] << 16);
+        hi[e] = (w[2 * e] >> 16) | (w[2 * e + 1] & 0xffff0000u);
       }
+      *(DAN_GLOBAL u32x4 *)(recb + kKtB + 2 * ((2 * dp) * kC + 8 * oc)) = lo;
+      *(DAN_GLOBAL u32x4 *)(recb + kKtB + 2 * ((2 * dp + 1) * kC + 8 * oc)) = hi;
     }
   }
-  __syncthreads();  // sG and the row factors
+  barrier_lds();  // sG, the row factors; every read of the tiles is done
+
+  // 3. L into the q tile's bytes, A staged in the k tile's (the record's A
+  //    block layout: bf16 hi and lo planes, or fp32).
 #pragma unroll
   for (int rr = 0; rr < 16; ++rr) {  // accumulator: row 8 (rr / 4) + 4 (lane / 32) + rr % 4, column lane % 32
     const int i = 32 * bi + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3), j = 32 * bj + (lane & 31);
     const float e = (i >= j && i < L) ? expf(sG[i] - sG[j]) : 0.f;
-    const float rkj = sL[j][kC + 2];
-    sL[i][j] = i > j ? sL[i][kC] * rkj * P[rr] * e : 0.f;
-    const float av = sL[i][kC + 1] * rkj * QK[rr] * e;
-    if constexpr (kBf) put_pair(kAhiB, kAloB, i * kC + j, av);
-    else Am[i * kC + j] = av;
+    const float rkj = sF[2][j];
+    sL[i][j] = i > j ? sF[0][i] * rkj * P[rr] * e : 0.f;
+    const float av = sF[1][i] * rkj * QK[rr] * e;
+    if constexpr (kBf) {
+      const __bf16 hi = (__bf16)av;
+      *reinterpret_cast<__bf16 *>(sKt + 2 * (i * kC + j)) = hi;
+      *reinterpret_cast<__bf16 *>(sKt + kC * kC * 2 + 2 * (i * kC + j)) = (__bf16)(av - (float)hi);
+    } else {
+      *reinterpret_cast<float *>(sKt + 4 * (i * kC + j)) = av;
+    }
   }
-  __syncthreads();
+  barrier_lds();
 
-  // T = (I + L)^-1 by forward substitution, x_i = [i == j] - sum_{m < i} L[i][m] x_m
-  // for column j: wave w solves columns 16 w .. 16 w + 15, four lanes per
-  // column (lane 4 c + p: column 16 w + c, the terms m = p mod 4), the four
-  // partial sums added by two quad swaps. Rows above 16 w are 0 in these
-  // columns; L[i][m] = 0 for m >= i, so whole groups of four are summed.
-  {
-    const int j = 16 * wave + (lane >> 2), part = lane & 3;
-    float xm[kC / 4];  // x_{4 k + part}
+  // 4. A out (16 KB from the stage), then T = (I + L)^-1 by forward
+  //    substitution, x_i = [i == j] - sum_{m < i} L[i][m] x_m for column j:
+  //    wave w solves columns 16 w .. 16 w + 15, four lanes per column (lane
+  //    4 c + p: column 16 w + c, the terms m = p mod 4), the four partial sums
+  //    added by two quad swaps. Rows above 16 w are 0 in these columns;
+  //    L[i][m] = 0 for m >= i, so whole groups of four are summed.
+  constexpr int kBlockBytes = kC * kC * 4;  // the T block, then the A block, of the record
+  static_assert(kAhiB == kBlockBytes && kThiB == 0, "record layout");
 #pragma unroll
-    for (int k = 0; k < kC / 4; ++k) xm[k] = 0.f;
+  for (int m = 0; m < kBlockBytes / (16 * kThreads); ++m) {
+    const int off = 16 * (kThreads * m + tid);
+    *(DAN_GLOBAL u32x4 *)(recb + kBlockBytes + off) = *reinterpret_cast<const u32x4 *>(sKt + off);
+  }
+  const int j = 16 * wave + (lane >> 2), part = lane & 3;
+  float xm[kC / 4];  // x_{4 k + part}
 #pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      if (i >= 16 * wave) {  // wave-uniform
-        float acc = 0.f;
+  for (int k = 0; k < kC / 4; ++k) xm[k] = 0.f;
+  switch (wave) {  // wave-uniform
+    case 0: tsolve_rows<0>(sL, xm, j, part); break;
+    case 1: tsolve_rows<1>(sL, xm, j, part); break;
+    case 2: tsolve_rows<2>(sL, xm, j, part); break;
+    default: tsolve_rows<3>(sL, xm, j, part); break;
+  }
+  barrier_lds();  // every wave's A reads of the stage are done
 #pragma unroll
-        for (int k = 0; k < (i + 3) / 4; ++k) acc = fmaf(sL[i][4 * k + part], xm[k], acc);
-        acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0xB1, 0xf, 0xf, false));
-        acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x4E, 0xf, 0xf, false));
-        const float xi = (i == j ? 1.f : 0.f) - acc;
-        if (part == (i & 3)) xm[i >> 2] = xi;
-      }
+  for (int k = 0; k < kC / 4; ++k) {
+    const int i = 4 * k + part;
+    if constexpr (kBf) {
+      const __bf16 hi = (__bf16)xm[k];
+      *reinterpret_cast<__bf16 *>(sKt + 2 * (i * kC + j)) = hi;
+      *reinterpret_cast<__bf16 *>(sKt + kC * kC * 2 + 2 * (i * kC + j)) = (__bf16)(xm[k] - (float)hi);
+    } else {
+      *reinterpret_cast<float *>(sKt + 4 * (i * kC + j)) = xm[k];
     }
+  }
+  barrier_lds();
 #pragma unroll
-    for (int k = 0; k < kC / 4; ++k) {
-      if constexpr (kBf) put_pair(kThiB, kTloB, (4 * k + part) * kC + j, xm[k]);
-      else Tm[(4 * k + part) * kC + j] = xm[k];
-    }
+  for (int m = 0; m < kBlockBytes / (16 * kThreads); ++m) {
+    const int off = 16 * (kThreads * m + tid);
+    *(DAN_GLOBAL u32x4 *)(recb + off) = *reinterpret_cast<const u32x4 *>(sKt + off);
   }
 }
 
@@ -295,10 +381,6 @@ constexpr int kScanLongWaves = 4, kScanShortWaves = 4;
 
 __device__ inline f32x4 mma(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
-// A work-group barrier that waits for this wave's LDS operations only:
-// __syncthreads() also waits for every global load in flight, which would
-// drain the next chunk's operand loads at each of the chunk's barriers.
-__device__ inline void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Contraction orders: the 128-long sums over the state rows take k-index
 // 32 (kk / 8) + 8 q + kk % 8 at step kk in lane group q = lane / 16 (a lane's
