@@ -33,9 +33,10 @@ extern "C" {
 
 /* Tokens per chunk of the chunked form. */
 #define DAN_GDN_CHUNK 64
-/* The chunked form walks calls whose runs average at most this many tokens
- * with a scan tuned for many short runs, other calls with one tuned for the
- * latency of long runs (same results). */
+/* For fp16 inputs the chunked form walks calls whose runs average at most
+ * this many tokens with a scan tuned for many short runs, other calls with
+ * one tuned for the latency of long runs (same results). bf16 inputs take
+ * the bf16-pair scan either way. */
 #define DAN_GDN_SHORT_RUN 256
 
 /* How dan_gdn_fwd walks a run. Both give the same recurrence within fp32

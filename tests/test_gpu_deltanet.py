@@ -74,27 +74,32 @@ def test_split_run_is_bit_identical(gpu):
     assert torch.equal(torch.cat([o1, o2]), out) and torch.equal(f2, fin)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("lengths", [[600, 1, 0, 700, 65], [40, 3, 64, 100, 17, 1]])
-def test_chunk_form_scan_variants(gpu, lengths):
-    """Calls whose runs average more than 256 tokens take the long-run scan
-    (16 state columns per work group), others the short-run one (32 columns;
-    DAN_GDN_SHORT_RUN); both against the recurrence, with ragged and empty
-    runs and GQA."""
-    say(f"delta rule, chunked form: runs {lengths} (mean {sum(lengths) / len(lengths):.0f})")
-    q, k, v, g, b, st = inputs(lengths, 1, 2, 128, torch.bfloat16, gpu, seed=11)
+def test_chunk_form_scan_variants(gpu, lengths, dtype):
+    """fp16 inputs: calls whose runs average more than 256 tokens take the
+    fp32 scan's long-run build (16 state columns per work group), others its
+    short-run one (32 columns; DAN_GDN_SHORT_RUN). bf16 inputs take the
+    bf16-pair scan either way. All against the recurrence, with ragged and
+    empty runs and GQA."""
+    say(f"delta rule, chunked form {dtype}: runs {lengths} (mean {sum(lengths) / len(lengths):.0f})")
+    q, k, v, g, b, st = inputs(lengths, 1, 2, 128, dtype, gpu, seed=11)
     out, fin = delta_rule(q, k, v, g, b, lengths, st, form="chunk")
     torch.cuda.synchronize()
     ref_o, ref_f = OD.delta_rule(*(x.cpu() for x in (q, k, v, g, b)), lengths, st.cpu(), recurrent=True)
-    check(out, fin, ref_o, ref_f, torch.bfloat16)
+    check(out, fin, ref_o, ref_f, dtype)
 
 
-def test_chunk_scan_variants_bit_identical(gpu):
-    """Two runs of 300 tokens average 300 (the long-run scan, 16 columns per
-    work group); with two empty runs appended they average 150 (the short-run
-    scan, 32 columns). Both builds add the same products in the same order,
-    so outputs and final states are bit-identical."""
-    say("delta rule, chunked form: long-run vs short-run scan on the same runs")
-    q, k, v, g, b, st = inputs([300, 300], 2, 2, 128, torch.bfloat16, gpu, seed=5)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_chunk_scan_variants_bit_identical(gpu, dtype):
+    """Two runs of 300 tokens average 300 (fp16: the fp32 scan's long-run
+    build, 16 columns per work group); with two empty runs appended they
+    average 150 (its short-run build, 32 columns). Both builds add the same
+    products in the same order, so outputs and final states are
+    bit-identical. bf16 (one scan for both) must not depend on empty runs
+    either."""
+    say(f"delta rule, chunked form {dtype}: long-run vs short-run scan on the same runs")
+    q, k, v, g, b, st = inputs([300, 300], 2, 2, 128, dtype, gpu, seed=5)
     o8, f8 = delta_rule(q, k, v, g, b, [300, 300], st, form="chunk")
     st4 = torch.cat([st, torch.zeros_like(st)])
     o4, f4 = delta_rule(q, k, v, g, b, [300, 300, 0, 0], st4, form="chunk")
