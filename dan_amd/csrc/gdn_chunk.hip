@@ -438,8 +438,20 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
 #pragma unroll
   for (int n = 0; n < NC; ++n) col[n] = 16 * (nb0 + n) + l16;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
-  for (int x = tid; x < kDk * kCols; x += 64 * W)
-    smem[(x / kCols) * kSS + x % kCols] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
+  {  // the state slice: every load in flight before the first LDS write
+    constexpr int kSt = kDk * kCols / (64 * W);
+    float sv[kSt];
+#pragma unroll
+    for (int m = 0; m < kSt; ++m) {
+      const int x = tid + 64 * W * m;
+      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
+    }
+#pragma unroll
+    for (int m = 0; m < kSt; ++m) {
+      const int x = tid + 64 * W * m;
+      smem[(x / kCols) * kSS + x % kCols] = sv[m];
+    }
+  }
   const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
   const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
   const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
@@ -607,8 +619,11 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
     cur ^= 1;
   }
   const float *sS = smem + cur * kDk * kSS;
-  for (int x = tid; x < kDk * kCols; x += 64 * W)
+#pragma unroll
+  for (int m = 0; m < kDk * kCols / (64 * W); ++m) {
+    const int x = tid + 64 * W * m;
     *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols) = sS[(x / kCols) * kSS + x % kCols];
+  }
 }
 
 // ---------------------------------------------------------------- the bf16 scan
@@ -701,14 +716,23 @@ void chunk_scan_bf16_kernel(const Params p) {
   const int rb = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col0 = COLS * cb;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
-  for (int x = tid; x < kDk * COLS; x += 256) {
-    const int row = x / COLS, c = x % COLS;
-    const float v = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)row * p.Dv + c);
-    sS[row * kSS + c] = v;
-    uint32_t hi, lo;
-    split_bf(v, hi, lo);
-    *reinterpret_cast<uint16_t *>(lds + LB::sHi + 2 * (c * kPS + row)) = (uint16_t)hi;
-    *reinterpret_cast<uint16_t *>(lds + LB::sLo + 2 * (c * kPS + row)) = (uint16_t)lo;
+  {  // the state slice: every load in flight before the first LDS write
+    constexpr int kSt = kDk * COLS / 256;
+    float sv[kSt];
+#pragma unroll
+    for (int m = 0; m < kSt; ++m) {
+      const int x = tid + 256 * m;
+      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / COLS) * p.Dv + x % COLS);
+    }
+#pragma unroll
+    for (int m = 0; m < kSt; ++m) {
+      const int x = tid + 256 * m, row = x / COLS, c = x % COLS;
+      sS[row * kSS + c] = sv[m];
+      uint32_t hi, lo;
+      split_bf(sv[m], hi, lo);
+      *reinterpret_cast<uint16_t *>(lds + LB::sHi + 2 * (c * kPS + row)) = (uint16_t)hi;
+      *reinterpret_cast<uint16_t *>(lds + LB::sLo + 2 * (c * kPS + row)) = (uint16_t)lo;
+    }
   }
   const int row0 = *(const DAN_GLOBAL int32_t *)(p.cu + r), end = *(const DAN_GLOBAL int32_t *)(p.cu + r + 1);
   const __bf16 *qh = static_cast<const __bf16 *>(p.q) + (int64_t)hk * p.q_sh;
@@ -889,8 +913,11 @@ void chunk_scan_bf16_kernel(const Params p) {
     load2(op, sn);
     barrier_lds();  // the new state is whole, and every read of this chunk's Y, D and S is done
   }
-  for (int x = tid; x < kDk * COLS; x += 256)
+#pragma unroll
+  for (int m = 0; m < kDk * COLS / 256; ++m) {
+    const int x = tid + 256 * m;
     *(DAN_GLOBAL float *)(p.s_out + sbase + (int64_t)(x / COLS) * p.Dv + x % COLS) = sS[(x / COLS) * kSS + x % COLS];
+  }
 }
 
 int64_t slots(int32_t num_tokens, int32_t num_runs) { return (int64_t)num_runs + num_tokens / kC; }
