@@ -367,14 +367,14 @@ def bench_gdn(args):
     init = torch.randn(len(trunks), hv, d, d, device=dev, generator=g) * 0.05
     trow = torch.cat([torch.arange(a, a + t) for a, t in trunks]).to(dev)
     brow = torch.cat([torch.arange(a, a + m) for a, m, _ in branches]).to(dev)
-    bseg = torch.tensor([i for _, _, i in branches], device=dev)
+    bseg = torch.tensor([i for _, _, i in branches], device=dev, dtype=torch.int32)  # the branch phase's state_index
     tl, bl = [t for _, t in trunks], [m for _, m, _ in branches]
     out = torch.empty(n, hv, d, dtype=torch.bfloat16, device=dev)
 
     def step():
         ot, ft = delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init)
         out[trow] = ot
-        ob, _ = delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, ft.index_select(0, bseg))
+        ob, _ = delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, ft, state_index=bseg)
         out[brow] = ob
 
     t_settle = time.perf_counter()  # the clock settles under sustained steps (see --settle-ms)
@@ -391,16 +391,17 @@ def bench_gdn(args):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t) / args.steps
     ft = delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init)[1]
-    bst = ft.index_select(0, bseg)
     tr_ms = _event_ms(lambda: delta_rule(q[trow], k[trow], v[trow], gate[trow], beta[trow], tl, init), args.steps)
-    br_ms = _event_ms(lambda: delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, bst), args.steps)
+    br_ms = _event_ms(lambda: delta_rule(q[brow], k[brow], v[brow], gate[brow], beta[brow], bl, ft, state_index=bseg),
+                      args.steps)
     forms = {}  # each phase's delta rule alone (inputs gathered beforehand), in each form
     tin = [x[trow] for x in (q, k, v, gate, beta)]
     bin_ = [x[brow] for x in (q, k, v, gate, beta)]
     for form in ("token", "chunk"):
         forms[form] = {
             "trunk_phase_ms": round(_event_ms(lambda: delta_rule(*tin, tl, init, form=form), args.steps), 4),
-            "branch_phase_ms": round(_event_ms(lambda: delta_rule(*bin_, bl, bst, form=form), args.steps), 4)}
+            "branch_phase_ms": round(_event_ms(lambda: delta_rule(*bin_, bl, ft, form=form, state_index=bseg),
+                                               args.steps), 4)}
     tokens = len(trow) + len(brow)
     flops = tokens * hv * 7 * d * d  # per token and head: decay, S^T k, the rank-1 write, S^T q
     layer = _gdn_layer_times(args, w, hk, hv, d, dev)

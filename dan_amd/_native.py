@@ -134,7 +134,7 @@ class DanFp8GemmArgs(ctypes.Structure):
                 ("w_scale", _vp), ("bias", _vp), ("y", _vp), ("y_stride", _i64)]
 
 
-GDN_ABI_VERSION = 3
+GDN_ABI_VERSION = 4
 GDN_FORM_TOKEN, GDN_FORM_CHUNK = 0, 1
 GDN_CHUNK = 64
 
@@ -147,7 +147,8 @@ class DanGdnArgs(ctypes.Structure):
                 ("v", _vp), ("v_stride_tok", _i64), ("v_stride_head", _i64),
                 ("g", _vp), ("beta", _vp), ("states_in", _vp), ("states_out", _vp),
                 ("out", _vp), ("o_stride_tok", _i64), ("o_stride_head", _i64),
-                ("workspace", _vp), ("workspace_bytes", _i64), ("form", _i32), ("reserved", _i32)]
+                ("workspace", _vp), ("workspace_bytes", _i64), ("form", _i32), ("reserved", _i32),
+                ("state_index", _vp), ("num_states_in", _i32), ("reserved2", _i32)]
 
 
 class DanGdnConvArgs(ctypes.Structure):

@@ -91,7 +91,8 @@ struct Params {
   float *s_out;
   void *o;
   float *norms;  // [N][Hk][2]: 1 / sqrt(sum q^2 + eps), 1 / sqrt(sum k^2 + eps)
-  int32_t N, Hk, Hv, Dv, R, cblocks;
+  const int32_t *sidx;  // NULL or [R]: run r's entry of s_in (clamped to [0, nsin))
+  int32_t N, Hk, Hv, Dv, R, cblocks, nsin;
 };
 
 // One wave per (token, key head): lanes 0-31 hold 4 values of q, 32-63 of k.
@@ -151,9 +152,11 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void gdn_kernel(const Params p
 
   // state rows kRows re .. kRows re + kRows - 1 of column c
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + c;
+  const int rin = p.sidx ? min(max(__builtin_amdgcn_readfirstlane(*(const DAN_GLOBAL int32_t *)(p.sidx + r)), 0), p.nsin - 1) : r;
+  const int64_t sbase_in = ((int64_t)rin * p.Hv + h) * kDk * p.Dv + c;
   float s[kRows];
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(kRows * re + i) * p.Dv);
+  for (int i = 0; i < kRows; ++i) s[i] = *(const DAN_GLOBAL float *)(p.s_in + sbase_in + (int64_t)(kRows * re + i) * p.Dv);
 
   const T *qh = static_cast<const T *>(p.q) + (int64_t)hk * p.q_sh;
   const T *kh = static_cast<const T *>(p.k) + (int64_t)hk * p.k_sh;
@@ -316,6 +319,8 @@ int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
       (a->k_stride_tok % 8) || (a->k_stride_head % 8))
     return fail(DAN_ERR_INVALID_ARGUMENT, "q and k rows must be 16-byte aligned");
   if (a->form != DAN_GDN_FORM_TOKEN && a->form != DAN_GDN_FORM_CHUNK) return fail(DAN_ERR_INVALID_ARGUMENT, "form %d", a->form);
+  if (a->state_index && a->num_states_in <= 0)
+    return fail(DAN_ERR_INVALID_ARGUMENT, "state_index needs num_states_in > 0, got %d", a->num_states_in);
   if (a->form == DAN_GDN_FORM_CHUNK && a->v_dim % 32)
     return fail(DAN_ERR_UNSUPPORTED, "v_dim %d: the chunked form takes a multiple of 32", a->v_dim);
   const int64_t need =
@@ -344,6 +349,7 @@ int dan_gdn_fwd(const DanGdnArgs *a, void *stream) {
   p.g = a->g; p.beta = a->beta; p.s_in = a->states_in; p.s_out = a->states_out; p.o = a->out;
   p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
   p.cblocks = a->v_dim / dan_gdn::kCols; p.N = a->num_tokens; p.norms = norms;
+  p.sidx = a->state_index; p.nsin = a->num_states_in;
   hipError_t err = dan_gdn::launch_norms(a, norms, s);
   if (err == hipSuccess) {
     const dim3 block(64 * dan_gdn::kWavesPerGroup);

@@ -85,8 +85,14 @@ struct Params {
   const float *g, *beta, *s_in;
   float *s_out, *rec;
   void *o;
-  int32_t Hk, Hv, Dv, R, ncb, units;
+  const int32_t *sidx;  // NULL or [R]: run r's entry of s_in (clamped to [0, nsin))
+  int32_t Hk, Hv, Dv, R, ncb, units, nsin;
 };
+
+// Run r's entry of s_in (wave-uniform).
+__device__ inline int state_in_of(const Params &p, int r) {
+  return p.sidx ? min(max(__builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(1))) int32_t *)(p.sidx + r)), 0), p.nsin - 1) : r;
+}
 
 template <typename T>
 __device__ inline f32x16 mfma_in(u32x4 a, u32x4 b, f32x16 c);
@@ -438,13 +444,14 @@ __global__ __launch_bounds__(64 * W) void chunk_scan_kernel(const Params p) {
 #pragma unroll
   for (int n = 0; n < NC; ++n) col[n] = 16 * (nb0 + n) + l16;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
+  const int64_t sbase_in = ((int64_t)state_in_of(p, r) * p.Hv + h) * kDk * p.Dv + col0;
   {  // the state slice: every load in flight before the first LDS write
     constexpr int kSt = kDk * kCols / (64 * W);
     float sv[kSt];
 #pragma unroll
     for (int m = 0; m < kSt; ++m) {
       const int x = tid + 64 * W * m;
-      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / kCols) * p.Dv + x % kCols);
+      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase_in + (int64_t)(x / kCols) * p.Dv + x % kCols);
     }
 #pragma unroll
     for (int m = 0; m < kSt; ++m) {
@@ -716,13 +723,14 @@ void chunk_scan_bf16_kernel(const Params p) {
   const int rb = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col0 = COLS * cb;
   const int64_t sbase = ((int64_t)r * p.Hv + h) * kDk * p.Dv + col0;
+  const int64_t sbase_in = ((int64_t)state_in_of(p, r) * p.Hv + h) * kDk * p.Dv + col0;
   {  // the state slice: every load in flight before the first LDS write
     constexpr int kSt = kDk * COLS / 256;
     float sv[kSt];
 #pragma unroll
     for (int m = 0; m < kSt; ++m) {
       const int x = tid + 256 * m;
-      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase + (int64_t)(x / COLS) * p.Dv + x % COLS);
+      sv[m] = *(const DAN_GLOBAL float *)(p.s_in + sbase_in + (int64_t)(x / COLS) * p.Dv + x % COLS);
     }
 #pragma unroll
     for (int m = 0; m < kSt; ++m) {
@@ -940,6 +948,7 @@ hipError_t dan_gdn_fwd_chunked(const DanGdnArgs *a, float *records, hipStream_t 
   p.rec = records;
   p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->v_dim; p.R = a->num_runs;
   p.units = a->num_runs * a->num_v_heads;
+  p.sidx = a->state_index; p.nsin = a->num_states_in;
   const int64_t prep = dan_gdnc::slots(a->num_tokens, a->num_runs) * a->num_v_heads;
   // Runs of DAN_GDN_SHORT_RUN tokens or fewer on average: the short-run scan;
   // longer: the long-run scan.

@@ -37,11 +37,14 @@ def _row_ok(t):
 CHUNK_MIN_RUN = 32
 
 
-def delta_rule(q, k, v, g, beta, lengths, states, cu=None, form=None):
+def delta_rule(q, k, v, g, beta, lengths, states, cu=None, form=None, state_index=None):
     """q, k [N, Hk, 128]; v [N, Hv, Dv] (bf16 or fp16, CUDA); g, beta [N, Hv];
     ``lengths``: run lengths summing to N (runs are consecutive rows);
-    ``states`` [R, Hv, 128, Dv] fp32. Returns (out [N, Hv, Dv] in q's dtype,
-    final states [R, Hv, 128, Dv] fp32). ``cu``: optional precomputed
+    ``states`` [R, Hv, 128, Dv] fp32, or with ``state_index`` ([R] integer,
+    on the device) [S, Hv, 128, Dv] of which run r starts from
+    ``states[state_index[r]]`` (``states.index_select(0, state_index)``
+    without the copy; an index outside [0, S) is clamped). Returns (out
+    [N, Hv, Dv] in q's dtype, final states [R, Hv, 128, Dv] fp32). ``cu``: optional precomputed
     (device, host) cumulative lengths, as dan passes them. ``form``: "token"
     (token by token: a run's results do not depend on how it is split into
     calls), "chunk" (64 tokens per step on the matrix cores, Dv a multiple of
@@ -60,8 +63,15 @@ def delta_rule(q, k, v, g, beta, lengths, states, cu=None, form=None):
         raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}: want [N, Hk, Dk], [N, Hv, Dv]")
     if sum(lengths) != n or any(x < 0 for x in lengths):
         raise ValueError(f"run lengths {list(lengths)[:8]}... must be >= 0 and sum to {n}")
-    if tuple(states.shape) != (r, hv, dk, dv):
+    if state_index is None and tuple(states.shape) != (r, hv, dk, dv):
         raise ValueError(f"states {tuple(states.shape)}: want {(r, hv, dk, dv)}")
+    if state_index is not None:
+        if states.dim() != 4 or tuple(states.shape[1:]) != (hv, dk, dv) or states.shape[0] < 1:
+            raise ValueError(f"states {tuple(states.shape)}: want (S >= 1, {hv}, {dk}, {dv}) with state_index")
+        if tuple(state_index.shape) != (r,) or state_index.device != q.device or state_index.dtype.is_floating_point:
+            raise ValueError(f"state_index {tuple(state_index.shape)} on {state_index.device}: want ({r},) integers "
+                             f"on {q.device}")
+        state_index = state_index.to(torch.int32).contiguous()
     if form is None:
         form = "chunk" if dv % 32 == 0 and max(lengths, default=0) >= CHUNK_MIN_RUN else "token"
     if form not in ("token", "chunk"):
@@ -97,6 +107,8 @@ def delta_rule(q, k, v, g, beta, lengths, states, cu=None, form=None):
     nbytes = _native.load().dan_gdn_workspace_size(code, n, r, hk, hv, dv)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     a.workspace, a.workspace_bytes, a.form = ws.data_ptr(), nbytes, code
+    if state_index is not None:
+        a.state_index, a.num_states_in = state_index.data_ptr(), s_in.shape[0]
     _native.gdn(a, torch.cuda.current_stream(dev).cuda_stream)
     return out, finals
 
@@ -305,24 +317,24 @@ class DeltaNet(nn.Module):
         out = torch.empty(n, self.hv, self.dv, device=x.device, dtype=x.dtype)
         final = self._phase(lay.trunk1, qkv, hist, b, a, init, out)
         if lay.trunk2 is not None:
-            f2 = self._phase(lay.trunk2, qkv, hist, b, a, final.index_select(0, lay.split_segments), out)
+            f2 = self._phase(lay.trunk2, qkv, hist, b, a, final, out, lay.split_segments)
             final_end = final.index_copy(0, lay.split_segments, f2)
         else:
             final_end = final
         for i, tail in lay.saves:  # prefix-cache entries at each save boundary
             segments[i].saved[self.index] = (_virtual_rows(qkv, hist, tail), final[i].clone())
         if lay.branches is not None:
-            self._phase(lay.branches, qkv, hist, b, a, final_end.index_select(0, lay.branch_segment), out)
+            self._phase(lay.branches, qkv, hist, b, a, final_end, out, lay.branch_segment)
         y = gated_rms_norm(out.reshape(-1, self.dv), z.reshape(-1, self.dv), self.norm.weight, self.eps)
         return self.out_proj(y.reshape(n, -1))
 
-    def _phase(self, ph, qkv, hist, b, a, states, out):
+    def _phase(self, ph, qkv, hist, b, a, states, out, state_index=None):
         conv, beta, g = conv_phase(qkv, hist, ph, self.conv1d.weight, b, a, self.A_log, self.dt_bias)
         t, kd = conv.shape[0], self.hk * self.dk
         q = conv[:, :kd].view(t, self.hk, self.dk)
         k = conv[:, kd:2 * kd].view(t, self.hk, self.dk)
         v = conv[:, 2 * kd:].view(t, self.hv, self.dv)
-        o, f = delta_rule(q, k, v, g, beta, ph.lens, states, ph.cu)
+        o, f = delta_rule(q, k, v, g, beta, ph.lens, states, ph.cu, state_index=state_index)
         out.index_copy_(0, ph.rows_long, o)
         return f
 

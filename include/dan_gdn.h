@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DAN_GDN_ABI_VERSION 3
+#define DAN_GDN_ABI_VERSION 4
 
 /* Tokens per chunk of the chunked form. */
 #define DAN_GDN_CHUNK 64
@@ -63,7 +63,7 @@ typedef struct {
   const void *v; int64_t v_stride_tok, v_stride_head; /* [N, Hv, Dv] */
   const float *g;    /* [N, Hv] log decay, row stride Hv */
   const float *beta; /* [N, Hv] write strength, row stride Hv */
-  const float *states_in; /* [R, Hv, Dk, Dv] */
+  const float *states_in; /* [R, Hv, Dk, Dv] ([num_states_in, ...] with state_index) */
   float *states_out;      /* [R, Hv, Dk, Dv] (may equal states_in) */
   void *out; int64_t o_stride_tok, o_stride_head; /* [N, Hv, Dv] */
   /* Device scratch of at least dan_gdn_workspace_size(form, N, R, Hk, Hv, Dv)
@@ -72,6 +72,13 @@ typedef struct {
   void *workspace; int64_t workspace_bytes;
   int32_t form;     /* DanGdnForm */
   int32_t reserved; /* 0 */
+  /* (GDN ABI 4) NULL, or [R] int32 on the device: run r starts from
+   * states_in[state_index[r]] of num_states_in entries (an index outside
+   * [0, num_states_in) is clamped), the gather of dan/models/qwen3_5.py:204
+   * and :211 done in the state load; states_out must not overlap states_in. */
+  const int32_t *state_index;
+  int32_t num_states_in;
+  int32_t reserved2; /* 0 */
 } DanGdnArgs;
 
 /* The gated delta rule over every run, from states_in to states_out.

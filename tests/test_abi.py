@@ -384,6 +384,8 @@ def _gdn_ptrs(**kw):
     (dict(form=_native.GDN_FORM_CHUNK, v_dim=40), _native.ERR_UNSUPPORTED, "multiple of 32"),
     (dict(form=_native.GDN_FORM_CHUNK, workspace_bytes=4096), _native.ERR_INVALID_ARGUMENT, "workspace needs"),
     (dict(form=_native.GDN_FORM_TOKEN, workspace_bytes=1024), _native.ERR_INVALID_ARGUMENT, "workspace needs"),
+    (dict(form=_native.GDN_FORM_CHUNK, state_index=4096, num_states_in=0), _native.ERR_INVALID_ARGUMENT,
+     "num_states_in"),
 ])
 def test_gdn_form_and_workspace_errors(lib, kw, status, needle):
     rc = lib.dan_gdn_fwd(ctypes.byref(_gdn_ptrs(**kw)), None)

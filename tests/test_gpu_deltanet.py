@@ -230,3 +230,22 @@ def test_c3_tree_phases_match_oracle(gpu, form):
     torch.cuda.synchronize()
     check(ot, ft, rt_o, rt_f, torch.bfloat16)
     check(ob, fb, rb_o, rb_f, torch.bfloat16)
+
+
+@pytest.mark.parametrize("form", ["token", "chunk"])
+def test_state_index_equals_gathered_states(gpu, form):
+    """Runs that start from states[state_index[r]] (the phase gather of
+    dan/models/qwen3_5.py:204 and :211 done in the kernels' state load) give
+    bit-identical outputs and final states to a call on the gathered states;
+    indices outside [0, S) are clamped to the nearest entry."""
+    say(f"delta rule {form}: state_index against gathered states")
+    lengths = [70, 5, 0, 130, 33]
+    q, k, v, g, b, _ = inputs(lengths, 2, 4, 128, torch.bfloat16, gpu, seed=21)
+    gen = torch.Generator().manual_seed(22)
+    pool = (torch.randn(3, 4, 128, 128, generator=gen) * 0.05).to(gpu)
+    idx = torch.tensor([2, 0, 2, -1, 5], dtype=torch.int64)
+    want_idx = idx.clamp(0, 2)
+    o1, f1 = delta_rule(q, k, v, g, b, lengths, pool, form=form, state_index=idx.to(gpu))
+    o2, f2 = delta_rule(q, k, v, g, b, lengths, pool.index_select(0, want_idx.to(gpu)), form=form)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(f1, f2)
